@@ -1,0 +1,391 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X attention hot path on BASELINE.json's configurations.
+
+Headline (`value`): config 3, Qwen3-8B-shape batched decode attention (B=32,
+32 q / 8 kv heads, D=128, bf16 cache, per-sequence lengths L_i ~ U{512..4096}
+seeded, one new token per sequence, so each sequence attends L_i+1 rows),
+reported as algorithmic KV-read GB/s: sum_b (L_b+1) * Hkv * D * 2 (K and V) *
+2 bytes (+ q and out) per step, over the measured step time.  One step = one
+decode-attention launch over the whole batch, inputs resident in HBM.  Three
+copies of the cache are rotated so the 256 MB Infinity Cache cannot serve a
+step from the previous step's reads.
+
+Also reported in the same line: config 4 (Qwen2.5-7B-shape causal prefill,
+B=8, S=4096, 28/4 heads) in TFLOP/s, algorithmic flops 4*D*Hq*B*S(S+1)/2; the
+fused QK-norm/RoPE/KV-append kernel at config 2 and config 3; and the CPU
+baseline (the C restatement of Crane's candle-CPU op chain, tests' oracle)
+timed on the host on a bounded sample of the same workloads.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--only decode|prefill|append]
+       [--no-cpu-baseline]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+import numpy as np
+
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, GB/s
+BF16_PEAK_TFLOPS = 2500.0      # MI355X dense bf16 MFMA, TFLOP/s
+METRIC = "decode attn KV GB/s (% of HBM peak) + prefill attn TFLOP/s, Qwen3-8B shape"
+SEED0 = 0xC3A7E000
+D = 128
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def c3_lengths() -> np.ndarray:
+    return np.random.Generator(np.random.PCG64(SEED0 + 3)).integers(512, 4096, size=32, endpoint=True).astype(np.int32)
+
+
+def randn(shape, gen, dtype, device, std=1.0):
+    import torch
+    t = torch.randn(shape, generator=gen, dtype=torch.float32, device=device)
+    if std != 1.0:
+        t.mul_(std)
+    return t.to(dtype)
+
+
+def timed(launch, steps: int, warmup: int, stream):
+    """Run `launch(i)` warmup + steps times; returns ms per step over the timed
+    steps, bracketed by synchronize and measured with events on `stream`."""
+    import torch
+    for i in range(warmup):
+        launch(i)
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for i in range(steps):
+        launch(warmup + i)
+    end.record(stream)
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / steps
+
+
+def cpu_info():
+    threads = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or len(os.sched_getaffinity(0))
+    model = "unknown"
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return threads, model
+
+
+# ---------------------------------------------------------------- decode
+
+def bench_decode(args, dev, stream, lib):
+    import torch
+    lens = c3_lengths()
+    B, Hq, Hkv = 32, 32, 8
+    kv_len = lens + 1                      # the new token is already appended
+    cap = int(kv_len.max())
+    R = 3
+    gen = torch.Generator(device=dev).manual_seed(SEED0 + 3)
+    ks = [randn((B, Hkv, cap, D), gen, torch.bfloat16, dev) for _ in range(R)]
+    vs = [randn((B, Hkv, cap, D), gen, torch.bfloat16, dev) for _ in range(R)]
+    q = randn((B, Hq, D), gen, torch.bfloat16, dev)
+    out = torch.empty((B, 1, Hq * D), dtype=torch.bfloat16, device=dev)
+    kv_len_d = torch.as_tensor(kv_len, device=dev)
+    need = lib.crane_hip_attn_decode_workspace(B, Hq, Hkv, D, cap, 1)
+    ws = torch.zeros(need, dtype=torch.uint8, device=dev)
+    scale = 1.0 / math.sqrt(D)
+    st = stream.cuda_stream
+    qp, op, lp, wp = q.data_ptr(), out.data_ptr(), kv_len_d.data_ptr(), ws.data_ptr()
+    kps = [k.data_ptr() for k in ks]
+    vps = [v.data_ptr() for v in vs]
+    fn = lib.crane_hip_attn_decode
+
+    def launch(i):
+        rc = fn(qp, kps[i % R], vps[i % R], cap, lp, cap, B, Hq, Hkv, D, scale, wp, need, op, 1, st)
+        if rc:
+            raise RuntimeError(f"crane_hip_attn_decode failed: {rc}")
+
+    ms = timed(launch, args.steps, args.warmup, stream)
+    kv_bytes = int(kv_len.sum()) * Hkv * D * 2 * 2
+    algo_bytes = kv_bytes + 2 * B * Hq * D * 2
+    gbs = algo_bytes / (ms * 1e-3) / 1e9
+    log(f"[decode c3] {ms * 1e3:.2f} us/step, {gbs:.1f} GB/s algorithmic ({gbs / HBM_PEAK_GBS * 100:.1f}% of HBM)")
+    data = dict(ms=ms, gbs=gbs, algo_bytes=algo_bytes, kv_bytes=kv_bytes, lens=lens, kv_len=kv_len,
+                B=B, Hq=Hq, Hkv=Hkv, cap=cap)
+    data["_tensors"] = (q, ks[0], vs[0], kv_len)
+    return data
+
+
+def bench_decode_c5(args, dev, stream, lib):
+    """Config 5 (Qwen2.5-72B shape, one layer, B=8, 64/8 heads, 32768-token cache,
+    K/V ~ N(0, 0.5)): reported beside the headline."""
+    import torch
+    B, Hq, Hkv, L = 8, 64, 8, 32768
+    kv_len = np.full(B, L + 1, np.int32)
+    cap = L + 1
+    gen = torch.Generator(device=dev).manual_seed(SEED0 + 5)
+    R = 2                                   # 2 x 1.07 GB: far beyond the 256 MB MALL
+    ks = [randn((B, Hkv, cap, D), gen, torch.bfloat16, dev, math.sqrt(0.5)) for _ in range(R)]
+    vs = [randn((B, Hkv, cap, D), gen, torch.bfloat16, dev, math.sqrt(0.5)) for _ in range(R)]
+    q = randn((B, Hq, D), gen, torch.bfloat16, dev)
+    out = torch.empty((B, 1, Hq * D), dtype=torch.bfloat16, device=dev)
+    kv_len_d = torch.as_tensor(kv_len, device=dev)
+    need = lib.crane_hip_attn_decode_workspace(B, Hq, Hkv, D, cap, 1)
+    ws = torch.zeros(need, dtype=torch.uint8, device=dev)
+    st = stream.cuda_stream
+    fn = lib.crane_hip_attn_decode
+
+    def launch(i):
+        rc = fn(q.data_ptr(), ks[i % R].data_ptr(), vs[i % R].data_ptr(), cap, kv_len_d.data_ptr(), cap, B, Hq, Hkv,
+                D, 1.0 / math.sqrt(D), ws.data_ptr(), need, out.data_ptr(), 1, st)
+        if rc:
+            raise RuntimeError(f"crane_hip_attn_decode failed: {rc}")
+
+    ms = timed(launch, max(3, args.steps // 2), args.warmup, stream)
+    algo = int(kv_len.sum()) * Hkv * D * 2 * 2 + 2 * B * Hq * D * 2
+    gbs = algo / (ms * 1e-3) / 1e9
+    log(f"[decode c5] {ms * 1e3:.2f} us/step, {gbs:.1f} GB/s ({gbs / HBM_PEAK_GBS * 100:.1f}% of HBM)")
+    del ks, vs
+    torch.cuda.empty_cache()
+    return dict(ms=ms, gbs=gbs, algo_bytes=algo)
+
+
+# ---------------------------------------------------------------- prefill
+
+def bench_prefill(args, dev, stream, lib):
+    import torch
+    B, S, Hq, Hkv = 8, 4096, 28, 4
+    gen = torch.Generator(device=dev).manual_seed(SEED0 + 4)
+    q = randn((B, Hq, S, D), gen, torch.bfloat16, dev)
+    k = randn((B, Hkv, S, D), gen, torch.bfloat16, dev)
+    v = randn((B, Hkv, S, D), gen, torch.bfloat16, dev)
+    out = torch.empty((B, S, Hq * D), dtype=torch.bfloat16, device=dev)
+    start = torch.zeros(B, dtype=torch.int32, device=dev)
+    st = stream.cuda_stream
+    fn = lib.crane_hip_attn_prefill
+
+    def launch(i):
+        rc = fn(q.data_ptr(), k.data_ptr(), v.data_ptr(), S, start.data_ptr(), 0, B, S, Hq, Hkv, D,
+                1.0 / math.sqrt(D), 1, out.data_ptr(), 1, st)
+        if rc:
+            raise RuntimeError(f"crane_hip_attn_prefill failed: {rc}")
+
+    ms = timed(launch, max(3, args.steps // 2), max(2, args.warmup // 2), stream)
+    flops = 4.0 * D * Hq * B * S * (S + 1) / 2
+    tflops = flops / (ms * 1e-3) / 1e12
+    log(f"[prefill c4] {ms:.3f} ms/step, {tflops:.1f} TFLOP/s ({tflops / BF16_PEAK_TFLOPS * 100:.1f}% of bf16 peak)")
+    return dict(ms=ms, tflops=tflops, flops=flops, B=B, S=S, Hq=Hq, Hkv=Hkv, _tensors=(q, k, v))
+
+
+def bench_prefill_c2(args, dev, stream, lib):
+    """Config 2 (Qwen3-0.6B-shape prefill, B=1, S=2048, 16/8 heads): fused
+    QK-norm + RoPE append into an empty cap-4096 cache, then causal prefill."""
+    import torch
+    B, S, Hq, Hkv, cap = 1, 2048, 16, 8, 4096
+    gen = torch.Generator(device=dev).manual_seed(SEED0 + 2)
+    qkv = randn((B, S, (Hq + 2 * Hkv) * D), gen, torch.bfloat16, dev)
+    from crane_amd import ops
+    cos, sin = ops.rope_tables(D, 1e6, 40960, device=dev, dtype=torch.bfloat16)
+    kc = torch.zeros((B, Hkv, cap, D), dtype=torch.bfloat16, device=dev)
+    vc = torch.zeros_like(kc)
+    q_out = torch.empty((B, Hq, S, D), dtype=torch.bfloat16, device=dev)
+    out = torch.empty((B, S, Hq * D), dtype=torch.bfloat16, device=dev)
+    zeros = torch.zeros(B, dtype=torch.int32, device=dev)
+    st = stream.cuda_stream
+    L = lib
+
+    def launch(i):
+        rc = L.crane_hip_qknorm_rope_append(qkv.data_ptr(), qkv.stride(1), None, None, 1e-6, 0, cos.data_ptr(),
+                                           sin.data_ptr(), cos.stride(0), cos.shape[0], zeros.data_ptr(),
+                                           q_out.data_ptr(), kc.data_ptr(), vc.data_ptr(), cap, zeros.data_ptr(),
+                                           S, B, S, Hq, Hkv, D, 1, st)
+        rc = rc or L.crane_hip_attn_prefill(q_out.data_ptr(), kc.data_ptr(), vc.data_ptr(), cap, zeros.data_ptr(), 0,
+                                            B, S, Hq, Hkv, D, 1.0 / math.sqrt(D), 1, out.data_ptr(), 1, st)
+        if rc:
+            raise RuntimeError(f"c2 step failed: {rc}")
+
+    ms = timed(launch, args.steps, args.warmup, stream)
+    flops = 4.0 * D * Hq * B * S * (S + 1) / 2
+    log(f"[prefill c2] append+prefill {ms * 1e3:.1f} us/step, {flops / (ms * 1e-3) / 1e12:.1f} TFLOP/s (launch-bound)")
+    return dict(ms=ms, tflops=flops / (ms * 1e-3) / 1e12)
+
+
+def bench_append(args, dev, stream, lib):
+    """Fused QK-norm + RoPE + KV append at config 4's prefill size (8 x 4096
+    tokens, 28/4 heads, rope only) and config 3's decode step (32 tokens)."""
+    import torch
+    from crane_amd import ops
+    res = {}
+    cos, sin = ops.rope_tables(D, 1e6, 40960, device=dev, dtype=torch.bfloat16)
+    st = stream.cuda_stream
+    for name, (B, S, Hq, Hkv, order, start) in {
+            "c4_prefill_append": (8, 4096, 28, 4, 2, 0),
+            "c3_decode_append": (32, 1, 32, 8, 0, 4096)}.items():
+        gen = torch.Generator(device=dev).manual_seed(SEED0 + 40)
+        qkv = randn((B, S, (Hq + 2 * Hkv) * D), gen, torch.bfloat16, dev)
+        cap = start + S
+        kc = torch.zeros((B, Hkv, cap, D), dtype=torch.bfloat16, device=dev)
+        vc = torch.zeros_like(kc)
+        q_out = torch.empty((B, Hq, S, D), dtype=torch.bfloat16, device=dev)
+        pos = torch.full((B,), start, dtype=torch.int32, device=dev)
+        w = torch.ones(D, dtype=torch.bfloat16, device=dev)
+
+        def launch(i):
+            rc = lib.crane_hip_qknorm_rope_append(
+                qkv.data_ptr(), qkv.stride(1), w.data_ptr(), w.data_ptr(), 1e-6, order, cos.data_ptr(),
+                sin.data_ptr(), cos.stride(0), cos.shape[0], pos.data_ptr(), q_out.data_ptr(), kc.data_ptr(),
+                vc.data_ptr(), cap, pos.data_ptr(), cap, B, S, Hq, Hkv, D, 1, st)
+            if rc:
+                raise RuntimeError(f"append failed: {rc}")
+
+        ms = timed(launch, args.steps, args.warmup, stream)
+        nbytes = B * S * (Hq + 2 * Hkv) * D * 2 * 2   # read qkv once, write q and the cache rows once
+        res[name] = dict(us=ms * 1e3, gbs=nbytes / (ms * 1e-3) / 1e9, bytes=nbytes)
+        log(f"[append {name}] {ms * 1e3:.1f} us, {nbytes / (ms * 1e-3) / 1e9:.0f} GB/s")
+    return res
+
+
+# ----------------------------------------------------------- CPU baseline
+
+def cpu_baseline(dec, pre):
+    """The oracle (C restatement of Crane's candle-CPU path, bf16 rounding
+    points) on the host cores, on bounded samples of configs 3 and 4."""
+    import torch
+    sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+    import oracle
+    threads, model = cpu_info()
+    res = {}
+    if dec is not None:
+        q, k, v, kv_len = dec["_tensors"]
+        nb = 8                                             # first 8 of the 32 sequences
+        qn = q[:nb].float().cpu().numpy()
+        kn = np.ascontiguousarray(k[:nb].float().cpu().numpy())
+        vn = np.ascontiguousarray(v[:nb].float().cpu().numpy())
+        lens = np.ascontiguousarray(kv_len[:nb])
+        times = []
+        t_end = time.time() + 15.0
+        while len(times) < 5 and (time.time() < t_end or not times):
+            t0 = time.perf_counter()
+            oracle.attn_decode(qn, kn, vn, lens, 1.0 / math.sqrt(D), "bf16", oracle.DECODE_GROUPED, threads)
+            times.append(time.perf_counter() - t0)
+        t = float(np.median(times))
+        nbytes = int(lens.sum()) * dec["Hkv"] * D * 2 * 2 + 2 * nb * dec["Hq"] * D * 2
+        res["decode"] = dict(value=nbytes / t / 1e9, unit="GB/s", cores=threads, kind="port",
+                             sample=f"config 3, sequences 0-7 of 32 (sum L={int(lens.sum())}), bf16 op chain, "
+                                    f"median of {len(times)} runs, {t * 1e3:.1f} ms each; host {model}")
+        log(f"[cpu decode] {res['decode']['value']:.2f} GB/s on {threads} threads")
+    if pre is not None:
+        q, k, v = pre["_tensors"]
+        S, Hq = pre["S"], pre["Hq"]
+        qn = np.ascontiguousarray(q[:1].float().cpu().numpy())
+        kn = np.ascontiguousarray(k[:1].float().cpu().numpy())
+        vn = np.ascontiguousarray(v[:1].float().cpu().numpy())
+        rows = [(S - 16, S)]                                # 16 heaviest rows, all heads of sequence 0
+        t0 = time.perf_counter()
+        flops = 0.0
+        for r0, r1 in rows:
+            oracle.attn_prefill(qn, kn, vn, np.zeros(1, np.int32), 1.0 / math.sqrt(D), True, "bf16",
+                                rows=(r0, r1), nthreads=threads)
+            flops += sum(4.0 * D * (i + 1) for i in range(r0, r1)) * Hq
+        t = time.perf_counter() - t0
+        res["prefill"] = dict(value=flops / t / 1e12, unit="TFLOP/s", cores=threads, kind="port",
+                              sample=f"config 4, sequence 0, rows {rows[0][0]}-{rows[0][1] - 1} x {Hq} heads "
+                                     f"(causal flops counted), bf16 op chain, {t:.1f} s; host {model}")
+        log(f"[cpu prefill] {res['prefill']['value'] * 1e3:.3f} GFLOP/s on {threads} threads")
+    return res
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--only", choices=["decode", "prefill", "append", "all"], default="all")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU: the attention path runs on a single MI355X and this build "
+              "launches nothing on a second GPU (see the sharding notes in DESIGN.md). Use --gpus 1.",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    from crane_amd import _lib
+    lib = _lib.lib()
+    if not torch.cuda.is_available():
+        print("bench.py needs a ROCm GPU", file=sys.stderr)
+        sys.exit(1)
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    stream = torch.cuda.current_stream(dev)
+    log(f"device: {torch.cuda.get_device_name(dev)}; lib: {_lib.version()}")
+
+    dec = pre = c5 = c2 = app = None
+    if args.only in ("decode", "all"):
+        dec = bench_decode(args, dev, stream, lib)
+        if args.only == "all":
+            c5 = bench_decode_c5(args, dev, stream, lib)
+    if args.only in ("prefill", "all"):
+        pre = bench_prefill(args, dev, stream, lib)
+        if args.only == "all":
+            c2 = bench_prefill_c2(args, dev, stream, lib)
+    if args.only in ("append", "all"):
+        app = bench_append(args, dev, stream, lib)
+    cpu = {} if args.no_cpu_baseline else cpu_baseline(dec, pre)
+
+    line = {"metric": METRIC, "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+            "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+            "data": "synthetic (seeded N(0,1) q/K/V; lengths U{512..4096} seeded)"}
+    if dec is not None:
+        line.update({
+            "value": round(dec["gbs"], 2), "unit": "GB/s", "ms_per_step": round(dec["ms"], 5),
+            "config": {"workload": "c3: Qwen3-8B-shape batched decode attention, B=32, 32 q / 8 kv heads, "
+                                   "D=128, bf16 KV cache, L_i~U{512..4096} seeded (+1 new token each)",
+                       "batch": 32, "q_heads": 32, "kv_heads": 8, "head_dim": 128,
+                       "sum_kv_rows": int(dec["kv_len"].sum()), "kv_bytes_per_step": dec["kv_bytes"]},
+            "roofline": {"bound": "hbm", "achieved": round(dec["gbs"], 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": round(dec["gbs"] / HBM_PEAK_GBS, 4), "traffic": None,
+                         "kernel": "decode_split_kernel<bf16,4>", "algo_bytes_per_launch": dec["algo_bytes"]},
+        })
+    if pre is not None:
+        pre_obj = {"metric": "prefill attn TFLOP/s (c4: Qwen2.5-7B shape, B=8, S=4096, 28/4 heads, causal, bf16)",
+                   "value": round(pre["tflops"], 2), "unit": "TFLOP/s", "ms_per_step": round(pre["ms"], 4),
+                   "roofline": {"bound": "mfma", "achieved": round(pre["tflops"], 2), "peak": BF16_PEAK_TFLOPS,
+                                "unit": "TFLOP/s", "frac": round(pre["tflops"] / BF16_PEAK_TFLOPS, 4),
+                                "traffic": None, "kernel": "prefill_bf16_kernel<causal>",
+                                "algo_flops_per_launch": pre["flops"]}}
+        if "prefill" in cpu:
+            pre_obj["cpu_baseline"] = cpu["prefill"]
+        if dec is None:
+            line.update({"value": pre_obj["value"], "unit": "TFLOP/s", "ms_per_step": pre_obj["ms_per_step"],
+                         "config": {"workload": "c4: Qwen2.5-7B-shape causal prefill"},
+                         "roofline": pre_obj["roofline"]})
+        line["prefill"] = pre_obj
+    if c5 is not None:
+        line["decode_c5"] = {"workload": "c5: Qwen2.5-72B-shape decode, B=8, 64/8 heads, L=32768+1",
+                             "value": round(c5["gbs"], 2), "unit": "GB/s", "us_per_step": round(c5["ms"] * 1e3, 2),
+                             "frac": round(c5["gbs"] / HBM_PEAK_GBS, 4)}
+    if c2 is not None:
+        line["prefill_c2"] = {"workload": "c2: Qwen3-0.6B-shape append+causal prefill, S=2048, 16/8 heads",
+                              "us_per_step": round(c2["ms"] * 1e3, 2), "tflops": round(c2["tflops"], 2)}
+    if app is not None:
+        line["append"] = {k: {kk: (round(vv, 2) if isinstance(vv, float) else vv) for kk, vv in v.items()}
+                          for k, v in app.items()}
+        if dec is None and pre is None:
+            a = app["c4_prefill_append"]
+            line.update({"value": round(a["gbs"], 2), "unit": "GB/s", "ms_per_step": round(a["us"] / 1e3, 5),
+                         "config": {"workload": "fused QK-norm+RoPE+KV append, c4 prefill size"}})
+    if "decode" in cpu:
+        line["cpu_baseline"] = cpu["decode"]
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

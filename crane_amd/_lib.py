@@ -1,0 +1,74 @@
+"""ctypes binding of libcrane_hip.so, the C ABI declared in include/crane_hip.h.
+
+The library is the only compute path: there is no CPU fallback.  Loading
+fails loudly when the built library is missing.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libcrane_hip.so")
+
+F32, BF16 = 0, 1
+NORM_THEN_ROPE, ROPE_THEN_NORM, ROPE_ONLY = 0, 1, 2
+
+OK = 0
+E_INVALID, E_DTYPE, E_HEAD_DIM, E_GQA, E_CAPACITY, E_WORKSPACE, E_LAUNCH, E_ALIGN = range(1, 9)
+
+# Every symbol include/crane_hip.h declares, with its ctypes signature.
+_vp, _i32p, _i64, _i, _f, _sz = (ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64, ctypes.c_int,
+                                 ctypes.c_float, ctypes.c_size_t)
+SIGNATURES = {
+    "crane_hip_strerror": ([_i], ctypes.c_char_p),
+    "crane_hip_version": ([], ctypes.c_char_p),
+    "crane_hip_qknorm_rope_append": (
+        [_vp, _i64, _vp, _vp, _f, _i, _vp, _vp, _i64, _i64, _i32p, _vp, _vp, _vp, _i64, _i32p, _i64,
+         _i, _i, _i, _i, _i, _i, _vp], _i),
+    "crane_hip_attn_decode_workspace": ([_i, _i, _i, _i, _i64, _i], _sz),
+    "crane_hip_attn_decode": (
+        [_vp, _vp, _vp, _i64, _i32p, _i64, _i, _i, _i, _i, _f, _vp, _sz, _vp, _i, _vp], _i),
+    "crane_hip_attn_prefill": (
+        [_vp, _vp, _vp, _i64, _i32p, _i64, _i, _i, _i, _i, _i, _f, _i, _vp, _i, _vp], _i),
+}
+
+
+class CraneHipError(RuntimeError):
+    """A nonzero crane_hip status (the analogue of candle's `bail!`)."""
+
+    def __init__(self, code: int, what: str):
+        self.code = code
+        super().__init__(f"{what}: {strerror(code)} (code {code})")
+
+
+_lib = None
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise ImportError(
+                f"{LIB_PATH} is not built; run `python -m crane_amd.build` (hipcc, gfx950). "
+                "crane_amd has no CPU fallback.")
+        L = ctypes.CDLL(LIB_PATH)
+        for name, (args, res) in SIGNATURES.items():
+            fn = getattr(L, name)
+            fn.argtypes = args
+            fn.restype = res
+        _lib = L
+    return _lib
+
+
+def strerror(code: int) -> str:
+    return lib().crane_hip_strerror(code).decode()
+
+
+def check(code: int, what: str) -> None:
+    if code != OK:
+        raise CraneHipError(code, what)
+
+
+def version() -> str:
+    return lib().crane_hip_version().decode()

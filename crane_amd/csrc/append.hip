@@ -1,0 +1,161 @@
+// append.hip -- fused per-head QK-RMSNorm + RoPE + KV-cache append (gfx950).
+//
+// One pass over Crane's merged qkv rows replaces, per layer,
+//   qwen3/modeling.rs:382-404  qkv narrow + reshape/transpose(+contiguous copies)
+//   qwen3/modeling.rs:410-419  q_norm / k_norm (candle_nn::RmsNorm over D)
+//   qwen3/modeling.rs:422-423  candle_nn::rotary_emb::rope on q and k (rotate-half)
+//   qwen3/modeling.rs:313-332  update_kv_cache: slice_set of k and v at cache_seq_len
+// with the Hunyuan order (rope, then norm: hunyuan_dense/modeling.rs:541-555) and
+// the Qwen2.5 order (rope only: qwen2.rs:75-76) selected by `order`.
+//
+// Work item = one head row (128 elements) of one token: Hq query rows, Hkv key
+// rows and Hkv value rows per token.  16 lanes own an item; lane l holds dims
+// [4l, 4l+4) and their rotate-half partners [64+4l, 64+4l+4), so the rotation
+// is lane-local and the RMS sum is a 16-lane butterfly.  Norm and rotation run
+// in f32 and each output element is rounded to the storage type once.  Every
+// cache row is written exactly once; q lands in [B,Hq,S,D] for the attention
+// kernels.  HBM traffic per token: (Hq+2Hkv)*D elements read, the same written.
+#include "common.h"
+
+namespace crane {
+namespace {
+
+constexpr int kItemsPerBlock = 16;  // 256 threads / 16 lanes per item
+
+__device__ __forceinline__ float group16_sum(float v) {
+    v += __shfl_xor(v, 1, 16);
+    v += __shfl_xor(v, 2, 16);
+    v += __shfl_xor(v, 4, 16);
+    v += __shfl_xor(v, 8, 16);
+    return v;
+}
+
+template <typename T>
+__device__ __forceinline__ void rms_norm16(float (&x1)[4], float (&x2)[4], const T* w, int l, float eps) {
+    float ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) ss += x1[i] * x1[i] + x2[i] * x2[i];
+    ss = group16_sum(ss);
+    const float inv = 1.0f / sqrtf(ss * (1.0f / kHeadDim) + eps);
+    float w1[4] = {1.f, 1.f, 1.f, 1.f}, w2[4] = {1.f, 1.f, 1.f, 1.f};
+    if (w) {
+        load4(w + 4 * l, w1);
+        load4(w + 64 + 4 * l, w2);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        x1[i] = x1[i] * inv * w1[i];
+        x2[i] = x2[i] * inv * w2[i];
+    }
+}
+
+__device__ __forceinline__ void rope4(float (&x1)[4], float (&x2)[4], const float (&c)[4], const float (&s)[4]) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const float a = x1[i], b = x2[i];
+        x1[i] = a * c[i] - b * s[i];
+        x2[i] = a * s[i] + b * c[i];
+    }
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void qknorm_rope_append_kernel(
+    const T* __restrict__ qkv, int64_t row_stride, const T* __restrict__ qw, const T* __restrict__ kw,
+    float eps, int order, const T* __restrict__ cos_t, const T* __restrict__ sin_t, int64_t cs_stride,
+    int64_t table_rows, const int32_t* __restrict__ positions, T* __restrict__ q_out, T* __restrict__ k_cache,
+    T* __restrict__ v_cache, int64_t cap, const int32_t* __restrict__ cache_len, int S, int Hq, int Hkv,
+    int64_t n_items) {
+    const int64_t item = (int64_t)blockIdx.x * kItemsPerBlock + (threadIdx.x >> 4);
+    const int l = threadIdx.x & 15;
+    if (item >= n_items) return;  // whole 16-lane groups leave together
+    const int H = Hq + 2 * Hkv;
+    const int head = (int)(item % H);
+    const int64_t tok = item / H;
+    const int s = (int)(tok % S);
+    const int b = (int)(tok / S);
+
+    const T* src = qkv + tok * row_stride + (int64_t)head * kHeadDim;
+    float x1[4], x2[4];
+    load4(src + 4 * l, x1);
+    load4(src + 64 + 4 * l, x2);
+
+    if (head >= Hq + Hkv) {  // value row: straight into the cache
+        const int64_t row = (int64_t)cache_len[b] + s;
+        if (row < 0 || row >= cap) return;
+        T* dst = v_cache + (((int64_t)b * Hkv + (head - Hq - Hkv)) * cap + row) * kHeadDim;
+        store4(dst + 4 * l, x1);
+        store4(dst + 64 + 4 * l, x2);
+        return;
+    }
+    const bool is_q = head < Hq;
+    T* dst;
+    if (is_q) {
+        dst = q_out + (((int64_t)b * Hq + head) * S + s) * kHeadDim;
+    } else {
+        const int64_t row = (int64_t)cache_len[b] + s;
+        if (row < 0 || row >= cap) return;
+        dst = k_cache + (((int64_t)b * Hkv + (head - Hq)) * cap + row) * kHeadDim;
+    }
+    const T* w = is_q ? qw : kw;
+    const int64_t p = (int64_t)positions[b] + s;
+    if (p < 0 || p >= table_rows) return;  // no table row for this position: nothing is written
+    float c[4], sn[4];
+    load4(cos_t + p * cs_stride + 4 * l, c);
+    load4(sin_t + p * cs_stride + 4 * l, sn);
+
+    if (order == CRANE_HIP_NORM_THEN_ROPE) rms_norm16(x1, x2, w, l, eps);
+    rope4(x1, x2, c, sn);
+    if (order == CRANE_HIP_ROPE_THEN_NORM) rms_norm16(x1, x2, w, l, eps);
+
+    store4(dst + 4 * l, x1);
+    store4(dst + 64 + 4 * l, x2);
+}
+
+}  // namespace
+}  // namespace crane
+
+using namespace crane;
+
+extern "C" int crane_hip_qknorm_rope_append(const void* qkv, int64_t qkv_row_stride, const void* q_norm_w,
+                                            const void* k_norm_w, float eps, int order, const void* cos,
+                                            const void* sin, int64_t cs_stride, int64_t table_rows,
+                                            const int32_t* positions,
+                                            void* q_out, void* k_cache, void* v_cache, int64_t cache_cap,
+                                            const int32_t* cache_len, int64_t max_rows, int B, int S, int Hq,
+                                            int Hkv, int D, int dtype, void* stream) {
+    if (dtype != CRANE_HIP_F32 && dtype != CRANE_HIP_BF16) return CRANE_HIP_E_DTYPE;
+    if (D != kHeadDim) return CRANE_HIP_E_HEAD_DIM;
+    if (B < 0 || S < 0 || Hq <= 0 || Hkv <= 0) return CRANE_HIP_E_INVALID;
+    if (Hq % Hkv != 0) return CRANE_HIP_E_GQA;
+    if (order < CRANE_HIP_NORM_THEN_ROPE || order > CRANE_HIP_ROPE_ONLY) return CRANE_HIP_E_INVALID;
+    if (!(eps >= 0.0f)) return CRANE_HIP_E_INVALID;
+    if (cache_cap <= 0 || max_rows < 0 || max_rows > cache_cap) return CRANE_HIP_E_CAPACITY;
+    if ((int64_t)S > max_rows) return CRANE_HIP_E_CAPACITY;
+    if (B == 0 || S == 0) return CRANE_HIP_OK;
+    if (!qkv || !cos || !sin || !positions || !q_out || !k_cache || !v_cache || !cache_len)
+        return CRANE_HIP_E_INVALID;
+    if (qkv_row_stride < (int64_t)(Hq + 2 * Hkv) * D || cs_stride < D / 2 || table_rows <= 0)
+        return CRANE_HIP_E_INVALID;
+    if (qkv_row_stride % 4 != 0 || cs_stride % 4 != 0) return CRANE_HIP_E_ALIGN;
+    if (!aligned16(qkv) || !aligned16(cos) || !aligned16(sin) || !aligned16(q_out) || !aligned16(k_cache) ||
+        !aligned16(v_cache) || (q_norm_w && !aligned16(q_norm_w)) || (k_norm_w && !aligned16(k_norm_w)))
+        return CRANE_HIP_E_ALIGN;
+
+    const int64_t n_items = (int64_t)B * S * (Hq + 2 * Hkv);
+    const int64_t blocks = (n_items + kItemsPerBlock - 1) / kItemsPerBlock;
+    if (blocks > 0x7fffffffLL) return CRANE_HIP_E_INVALID;
+    hipStream_t st = (hipStream_t)stream;
+    if (dtype == CRANE_HIP_F32) {
+        hipLaunchKernelGGL(qknorm_rope_append_kernel<float>, dim3((unsigned)blocks), dim3(256), 0, st,
+                           (const float*)qkv, qkv_row_stride, (const float*)q_norm_w, (const float*)k_norm_w, eps,
+                           order, (const float*)cos, (const float*)sin, cs_stride, table_rows, positions, (float*)q_out,
+                           (float*)k_cache, (float*)v_cache, cache_cap, cache_len, S, Hq, Hkv, n_items);
+    } else {
+        hipLaunchKernelGGL(qknorm_rope_append_kernel<bf16_t>, dim3((unsigned)blocks), dim3(256), 0, st,
+                           (const bf16_t*)qkv, qkv_row_stride, (const bf16_t*)q_norm_w, (const bf16_t*)k_norm_w,
+                           eps, order, (const bf16_t*)cos, (const bf16_t*)sin, cs_stride, table_rows, positions,
+                           (bf16_t*)q_out, (bf16_t*)k_cache, (bf16_t*)v_cache, cache_cap, cache_len, S, Hq, Hkv,
+                           n_items);
+    }
+    return launch_status(hipGetLastError());
+}

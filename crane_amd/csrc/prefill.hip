@@ -1,0 +1,304 @@
+// prefill.hip -- causal GQA flash prefill over Crane's [B, Hkv, cap, D] cache (gfx950).
+//
+// Replaces the prefill SDPA of qwen3/modeling.rs:469-502 (K/V expanded to Hq
+// heads, (q@K^T)*scale, + the causal -1e9 mask of :866-884, softmax_last_dim,
+// @V, transpose to [B,S,Hq*D]); the same op chain is in
+// hunyuan_dense/modeling.rs:610-645 and qwen2.rs:191-211 (-inf mask).  The
+// [S, start+S] score matrix is never materialised: scores live in registers,
+// the softmax is online (running max and sum per query row, log2 domain) and
+// key tiles that lie entirely above the diagonal are never visited.
+//
+// bf16 kernel (MFMA): a workgroup owns 128 query rows of one q head (4 waves
+// x 32 rows).  Each wave computes S^T = K Q^T with v_mfma_f32_32x32x16_bf16,
+// so a lane holds 16 keys of ONE query row (lane%32) and the row max/sum need
+// one cross-half exchange only.  The resulting P^T tile is already laid out as
+// the B operand of O^T = V^T P^T: no data movement between the two products.
+// K is staged in LDS row-major ([key][dim], A operand of the first product);
+// V is staged transposed ([dim][key]) so that each A-operand fragment of the
+// second product is two 8-byte LDS reads.  LDS rows are padded to spread banks.
+// Workgroup ids are remapped so that heavy (late) query tiles start first and
+// the q heads sharing a kv head run on the same XCD (shared L2).
+//
+// f32 kernel: a plain wave-per-query-row online-softmax kernel; Crane serves
+// prefill in bf16 on GPU (crane-serve/src/lib.rs:123-150), f32 is kept for
+// completeness of the operator.
+#include "common.h"
+
+namespace crane {
+namespace {
+
+constexpr int kBM = 128;           // query rows per workgroup
+constexpr int kBN = 64;            // keys per tile
+constexpr int kKStride = 128 + 8;  // bf16 elements per K row in LDS (272 B)
+constexpr int kVStride = kBN + 4;  // bf16 elements per V^T row in LDS (136 B)
+
+__device__ __forceinline__ f32x16_v mfma32(bf16x8_v a, bf16x8_v b, f32x16_v c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ bf16x8_v as_bf16x8(uint4 u) { return __builtin_bit_cast(bf16x8_v, u); }
+
+// Map the 1-D workgroup id to (q tile, sequence, q head).  Groups of
+// 8*n_rep consecutive ids hold 8 (qtile, b, kv head) units x n_rep heads, laid
+// out so that ids congruent mod 8 (dispatched to the same XCD) share a unit.
+// Units are ordered heaviest (last q tile) first.  Returns false for padding ids.
+__device__ __forceinline__ bool map_block(int id, int n_qt, int B, int Hkv, int n_rep, int& qt, int& b, int& hq) {
+    const int chunk = 8 * n_rep;
+    const int c = id / chunk, rem = id % chunk;
+    const int r = rem / 8, x = rem % 8;
+    const int unit = c * 8 + x;
+    const int n_units = n_qt * B * Hkv;
+    if (unit >= n_units) return false;
+    const int qt_rank = unit / (B * Hkv);
+    const int rest = unit % (B * Hkv);
+    b = rest / Hkv;
+    const int kvh = rest % Hkv;
+    qt = n_qt - 1 - qt_rank;
+    hq = kvh * n_rep + r;
+    return true;
+}
+
+template <bool CAUSAL>
+__global__ __launch_bounds__(256) void prefill_bf16_kernel(
+    const bf16_t* __restrict__ q, const bf16_t* __restrict__ kc, const bf16_t* __restrict__ vc, int64_t cap,
+    const int32_t* __restrict__ start_pos, int max_start, int S, int B, int Hq, int Hkv, float scale_log2,
+    bf16_t* __restrict__ out) {
+    const int n_rep = Hq / Hkv;
+    const int n_qt = (S + kBM - 1) / kBM;
+    int qt, b, hq;
+    if (!map_block(blockIdx.x, n_qt, B, Hkv, n_rep, qt, b, hq)) return;
+    const int kvh = hq / n_rep;
+    const int start = min(max(start_pos[b], 0), max_start);
+    const int m0 = qt * kBM;
+
+    __shared__ __attribute__((aligned(16))) bf16_t k_lds[kBN * kKStride];
+    __shared__ __attribute__((aligned(16))) bf16_t vt_lds[kHeadDim * kVStride];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6;
+    const int n = lane & 31, hh = lane >> 5;
+
+    // Q fragments (B operand of S^T = K Q^T): query row qrow, dims 16ks + 8hh .. +7.
+    const int qrow = m0 + wave * 32 + n;
+    bf16x8_v qf[8];
+    {
+        const bf16_t* qp = q + (((int64_t)b * Hq + hq) * S + min(qrow, S - 1)) * kHeadDim + 8 * hh;
+#pragma unroll
+        for (int ks = 0; ks < 8; ++ks) {
+            uint4 u = *reinterpret_cast<const uint4*>(qp + 16 * ks);
+            if (qrow >= S) u = make_uint4(0, 0, 0, 0);
+            qf[ks] = as_bf16x8(u);
+        }
+    }
+    f32x16_v oacc[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) oacc[i][r] = 0.f;
+    float m_run = -INFINITY, l_run = 0.f;
+
+    const int L = start + S;                                     // keys in the cache for this chunk
+    const int kend = CAUSAL ? min(start + m0 + kBM, L) : L;      // keys any row of the tile can see
+    const int qpos = start + qrow;                               // absolute position of my query
+    const int wave_last = start + m0 + wave * 32 + 31;           // last position of this wave's rows
+    const bf16_t* Kg = kc + ((int64_t)b * Hkv + kvh) * cap * kHeadDim;
+    const bf16_t* Vg = vc + ((int64_t)b * Hkv + kvh) * cap * kHeadDim;
+
+    for (int kt = 0; kt < kend; kt += kBN) {
+        // ---- stage K tile [64 keys][128 dims] and V^T tile [128 dims][64 keys]
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int p = tid + 256 * i;
+            const int key = p >> 4, ch = p & 15;
+            uint4 u = make_uint4(0, 0, 0, 0);
+            if (kt + key < kend) u = *reinterpret_cast<const uint4*>(Kg + (int64_t)(kt + key) * kHeadDim + 8 * ch);
+            *reinterpret_cast<uint4*>(&k_lds[key * kKStride + 8 * ch]) = u;
+        }
+        {
+            const int a = tid >> 4, ch = tid & 15;  // keys 4a..4a+3, dims 8ch..8ch+7
+            uint4 v[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int key = kt + 4 * a + r;
+                v[r] = make_uint4(0, 0, 0, 0);
+                if (key < kend) v[r] = *reinterpret_cast<const uint4*>(Vg + (int64_t)key * kHeadDim + 8 * ch);
+            }
+            const uint32_t* w0 = reinterpret_cast<const uint32_t*>(&v[0]);
+            const uint32_t* w1 = reinterpret_cast<const uint32_t*>(&v[1]);
+            const uint32_t* w2 = reinterpret_cast<const uint32_t*>(&v[2]);
+            const uint32_t* w3 = reinterpret_cast<const uint32_t*>(&v[3]);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                // dim 8ch+2i (low halves) and 8ch+2i+1 (high halves) of the 4 keys
+                const uint2 lo = make_uint2((w0[i] & 0xffffu) | (w1[i] << 16), (w2[i] & 0xffffu) | (w3[i] << 16));
+                const uint2 hi = make_uint2((w0[i] >> 16) | (w1[i] & 0xffff0000u),
+                                            (w2[i] >> 16) | (w3[i] & 0xffff0000u));
+                *reinterpret_cast<uint2*>(&vt_lds[(8 * ch + 2 * i) * kVStride + 4 * a]) = lo;
+                *reinterpret_cast<uint2*>(&vt_lds[(8 * ch + 2 * i + 1) * kVStride + 4 * a]) = hi;
+            }
+        }
+        __syncthreads();
+
+        const bool wave_active = !CAUSAL || kt <= wave_last;
+        if (wave_active) {
+            // ---- S^T = K Q^T for the 64 keys: two 32x32 blocks
+            f32x16_v sacc[2];
+#pragma unroll
+            for (int nb = 0; nb < 2; ++nb) {
+#pragma unroll
+                for (int r = 0; r < 16; ++r) sacc[nb][r] = 0.f;
+#pragma unroll
+                for (int ks = 0; ks < 8; ++ks) {
+                    const uint4 ku = *reinterpret_cast<const uint4*>(&k_lds[(nb * 32 + n) * kKStride + 16 * ks + 8 * hh]);
+                    sacc[nb] = mfma32(as_bf16x8(ku), qf[ks], sacc[nb]);
+                }
+            }
+            // ---- online softmax for query row n (keys: 8*(r/4) + 4*hh + r%4 of block nb)
+            const bool need_mask = kt + kBN > kend || (CAUSAL && kt + kBN - 1 > start + m0 + wave * 32);
+            float tmax = -INFINITY;
+#pragma unroll
+            for (int nb = 0; nb < 2; ++nb)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    float s = sacc[nb][r] * scale_log2;
+                    if (need_mask) {
+                        const int key = kt + nb * 32 + 8 * (r >> 2) + 4 * hh + (r & 3);
+                        if (key >= kend || (CAUSAL && key > qpos)) s = -INFINITY;
+                    }
+                    sacc[nb][r] = s;
+                    tmax = fmaxf(tmax, s);
+                }
+            tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
+            const float m_new = fmaxf(m_run, tmax);
+            // m_new is finite: key 0 is visible to every query and tile 0 comes first
+            const float alpha = fast_exp2(m_run - m_new);
+            float psum = 0.f;
+            bf16x8_v pf[4];
+#pragma unroll
+            for (int nb = 0; nb < 2; ++nb)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const float p = fast_exp2(sacc[nb][r] - m_new);
+                    psum += p;
+                    pf[nb * 2 + (r >> 3)][r & 7] = (__bf16)p;
+                }
+            psum += __shfl_xor(psum, 32);
+            l_run = l_run * alpha + psum;
+            m_run = m_new;
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) oacc[i][r] *= alpha;
+            // ---- O^T += V^T P^T: 4 dim blocks x 4 key steps of 16
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+#pragma unroll
+                for (int db = 0; db < 4; ++db) {
+                    const bf16_t* vp = &vt_lds[(db * 32 + n) * kVStride + 16 * t + 4 * hh];
+                    const uint2 lo = *reinterpret_cast<const uint2*>(vp);
+                    const uint2 hi = *reinterpret_cast<const uint2*>(vp + 8);
+                    const uint4 vu = make_uint4(lo.x, lo.y, hi.x, hi.y);
+                    oacc[db] = mfma32(as_bf16x8(vu), pf[t], oacc[db]);
+                }
+            }
+        }
+        __syncthreads();
+    }
+
+    if (qrow < S) {
+        const float inv = 1.0f / l_run;
+        bf16_t* op = out + (((int64_t)b * S + qrow) * Hq + hq) * kHeadDim;
+#pragma unroll
+        for (int db = 0; db < 4; ++db)
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const int dim = db * 32 + 8 * g + 4 * hh;
+                const uint2 w = make_uint2(pack_bf16x2(oacc[db][4 * g] * inv, oacc[db][4 * g + 1] * inv),
+                                           pack_bf16x2(oacc[db][4 * g + 2] * inv, oacc[db][4 * g + 3] * inv));
+                *reinterpret_cast<uint2*>(op + dim) = w;
+            }
+    }
+}
+
+// f32: one wave per (query row, q head, sequence); lane owns dims 2*lane, 2*lane+1.
+template <bool CAUSAL>
+__global__ __launch_bounds__(64) void prefill_f32_kernel(const float* __restrict__ q, const float* __restrict__ kc,
+                                                         const float* __restrict__ vc, int64_t cap,
+                                                         const int32_t* __restrict__ start_pos, int max_start, int S,
+                                                         int Hq, int Hkv, float scale_log2, float* __restrict__ out) {
+    const int i = blockIdx.x, hq = blockIdx.y, b = blockIdx.z;
+    const int lane = threadIdx.x;
+    const int n_rep = Hq / Hkv, kvh = hq / n_rep;
+    const int start = min(max(start_pos[b], 0), max_start);
+    const int L = start + S;
+    const int kend = CAUSAL ? start + i + 1 : L;
+    const float2 qv = *reinterpret_cast<const float2*>(q + (((int64_t)b * Hq + hq) * S + i) * kHeadDim + 2 * lane);
+    const float* Kg = kc + ((int64_t)b * Hkv + kvh) * cap * kHeadDim + 2 * lane;
+    const float* Vg = vc + ((int64_t)b * Hkv + kvh) * cap * kHeadDim + 2 * lane;
+    float m = -INFINITY, l = 0.f, o0 = 0.f, o1 = 0.f;
+    for (int j = 0; j < kend; ++j) {
+        const float2 kv = *reinterpret_cast<const float2*>(Kg + (int64_t)j * kHeadDim);
+        float s = qv.x * kv.x + qv.y * kv.y;
+#pragma unroll
+        for (int msk = 32; msk >= 1; msk >>= 1) s += __shfl_xor(s, msk);
+        s *= scale_log2;
+        const float m_new = fmaxf(m, s);
+        const float alpha = fast_exp2(m - m_new), p = fast_exp2(s - m_new);
+        const float2 vv = *reinterpret_cast<const float2*>(Vg + (int64_t)j * kHeadDim);
+        l = l * alpha + p;
+        o0 = o0 * alpha + p * vv.x;
+        o1 = o1 * alpha + p * vv.y;
+        m = m_new;
+    }
+    float* op = out + (((int64_t)b * S + i) * Hq + hq) * kHeadDim + 2 * lane;
+    *reinterpret_cast<float2*>(op) = make_float2(o0 / l, o1 / l);
+}
+
+}  // namespace
+}  // namespace crane
+
+using namespace crane;
+
+extern "C" int crane_hip_attn_prefill(const void* q, const void* k_cache, const void* v_cache, int64_t cache_cap,
+                                      const int32_t* start_pos, int64_t max_start, int B, int S, int Hq, int Hkv,
+                                      int D, float scale, int causal, void* out, int dtype, void* stream) {
+    if (dtype != CRANE_HIP_F32 && dtype != CRANE_HIP_BF16) return CRANE_HIP_E_DTYPE;
+    if (D != kHeadDim) return CRANE_HIP_E_HEAD_DIM;
+    if (B < 0 || S < 0 || Hq <= 0 || Hkv <= 0 || max_start < 0) return CRANE_HIP_E_INVALID;
+    if (Hq % Hkv != 0) return CRANE_HIP_E_GQA;
+    if (!(scale > 0.0f) || !__builtin_isfinite(scale)) return CRANE_HIP_E_INVALID;
+    if (cache_cap <= 0 || max_start + (int64_t)S > cache_cap) return CRANE_HIP_E_CAPACITY;
+    if (B == 0 || S == 0) return CRANE_HIP_OK;
+    if (!q || !k_cache || !v_cache || !start_pos || !out) return CRANE_HIP_E_INVALID;
+    if (!aligned16(q) || !aligned16(k_cache) || !aligned16(v_cache) || !aligned16(out)) return CRANE_HIP_E_ALIGN;
+    if (cache_cap > 0x7fffffffLL || B > 65535 || Hq > 65535) return CRANE_HIP_E_INVALID;
+    hipStream_t st = (hipStream_t)stream;
+    const float sl = scale * kLog2e;
+    if (dtype == CRANE_HIP_BF16) {
+        const int n_rep = Hq / Hkv;
+        const int64_t n_qt = (S + kBM - 1) / kBM;
+        const int64_t units = n_qt * B * Hkv;
+        const int64_t chunk = 8LL * n_rep;
+        const int64_t blocks = ((units + 7) / 8) * chunk;
+        if (blocks > 0x7fffffffLL) return CRANE_HIP_E_INVALID;
+        if (causal)
+            hipLaunchKernelGGL(prefill_bf16_kernel<true>, dim3((unsigned)blocks), dim3(256), 0, st,
+                               (const bf16_t*)q, (const bf16_t*)k_cache, (const bf16_t*)v_cache, cache_cap, start_pos,
+                               (int)max_start, S, B, Hq, Hkv, sl, (bf16_t*)out);
+        else
+            hipLaunchKernelGGL(prefill_bf16_kernel<false>, dim3((unsigned)blocks), dim3(256), 0, st,
+                               (const bf16_t*)q, (const bf16_t*)k_cache, (const bf16_t*)v_cache, cache_cap, start_pos,
+                               (int)max_start, S, B, Hq, Hkv, sl, (bf16_t*)out);
+    } else {
+        const dim3 grid((unsigned)S, (unsigned)Hq, (unsigned)B);
+        if (causal)
+            hipLaunchKernelGGL(prefill_f32_kernel<true>, grid, dim3(64), 0, st, (const float*)q, (const float*)k_cache,
+                               (const float*)v_cache, cache_cap, start_pos, (int)max_start, S, Hq, Hkv, sl,
+                               (float*)out);
+        else
+            hipLaunchKernelGGL(prefill_f32_kernel<false>, grid, dim3(64), 0, st, (const float*)q,
+                               (const float*)k_cache, (const float*)v_cache, cache_cap, start_pos, (int)max_start, S,
+                               Hq, Hkv, sl, (float*)out);
+    }
+    return launch_status(hipGetLastError());
+}

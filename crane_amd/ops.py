@@ -1,0 +1,225 @@
+"""Tensor-in / Tensor-out host surface of the attention path.
+
+Mirrors the candle calls Crane makes inside Attention::forward
+(crane-core/src/models/qwen3/modeling.rs:372-503) and the operator
+conventions of its fused_ops plugin (crane-core/src/fused_ops/cuda_impl.rs:
+a bad shape/dtype raises, outputs are freshly allocated tensors, the KV cache
+is mutated in place like `slice_set`).  torch tensors on the ROCm device
+stand in for candle's device Tensor; every compute call goes through the C
+ABI of libcrane_hip.so.  Tensors not on a GPU are rejected: there is no CPU
+fallback.
+"""
+from __future__ import annotations
+
+import math
+from typing import Optional
+
+import torch
+
+from . import _lib
+from ._lib import CraneHipError, check
+
+_DTYPES = {torch.float32: _lib.F32, torch.bfloat16: _lib.BF16}
+_ORDERS = {"norm_then_rope": _lib.NORM_THEN_ROPE, "rope_then_norm": _lib.ROPE_THEN_NORM,
+           "rope_only": _lib.ROPE_ONLY}
+HEAD_DIM = 128
+
+
+def _dtype_code(t: torch.Tensor) -> int:
+    try:
+        return _DTYPES[t.dtype]
+    except KeyError:
+        raise CraneHipError(_lib.E_DTYPE, f"dtype {t.dtype}") from None
+
+
+def _dev(*ts: Optional[torch.Tensor]) -> torch.device:
+    dev = None
+    for t in ts:
+        if t is None:
+            continue
+        if t.device.type != "cuda":
+            raise CraneHipError(_lib.E_INVALID, f"tensor on {t.device}: crane_amd runs on the GPU only")
+        if dev is None:
+            dev = t.device
+        elif t.device != dev:
+            raise CraneHipError(_lib.E_INVALID, "tensors on different devices")
+    return dev
+
+
+def _contig(t: torch.Tensor, name: str) -> None:
+    if not t.is_contiguous():
+        raise CraneHipError(_lib.E_INVALID, f"{name} must be contiguous")
+
+
+def _i32(t: torch.Tensor, n: int, name: str) -> None:
+    if t.dtype != torch.int32 or t.numel() != n or not t.is_contiguous():
+        raise CraneHipError(_lib.E_INVALID, f"{name} must be a contiguous int32 tensor of {n} elements")
+
+
+def _stream(dev: torch.device) -> int:
+    return torch.cuda.current_stream(dev).cuda_stream
+
+
+def _ptr(t: Optional[torch.Tensor]) -> Optional[int]:
+    return None if t is None else t.data_ptr()
+
+
+# ---------------------------------------------------------------- rope tables
+
+def rope_tables(head_dim: int, theta: float, max_pos: int, alpha: float = 0.0,
+                device: torch.device | str = "cuda", dtype: torch.dtype = torch.float32):
+    """cos/sin tables [max_pos, head_dim/2] following qwen3/modeling.rs:117-139
+    (inv_freq = 1.0f32 / (f32)(base^(2i/d)) with the power in f64; f32 products;
+    cos/sin in f32) and the Hunyuan NTK-alpha base of
+    hunyuan_dense/modeling.rs:202-219, then cast to the model dtype as
+    qwen3/modeling.rs:857-864 does.  Built once per model, like the reference."""
+    base = float(theta)
+    if alpha and alpha > 0.0:
+        base = theta * alpha ** (head_dim / (head_dim - 2.0))
+    # f64 power, cast to f32, then an f32 reciprocal
+    powers = torch.tensor([base ** (i / head_dim) for i in range(0, head_dim, 2)], dtype=torch.float64)
+    inv = torch.ones((), dtype=torch.float32) / powers.to(torch.float32)
+    pos = torch.arange(max_pos, dtype=torch.float32)
+    freqs = (pos[:, None] * inv[None, :]).to(device)
+    return freqs.cos().to(dtype).contiguous(), freqs.sin().to(dtype).contiguous()
+
+
+# ------------------------------------------------------------ fused append op
+
+def qk_norm_rope_append(qkv: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,
+                        positions: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
+                        cache_len: torch.Tensor, max_rows: int, num_heads: int, num_kv_heads: int,
+                        q_norm_w: Optional[torch.Tensor] = None,
+                        k_norm_w: Optional[torch.Tensor] = None, eps: float = 1e-6,
+                        order: str = "norm_then_rope") -> torch.Tensor:
+    """Per-head QK-RMSNorm + RoPE, K/V written into the cache at rows
+    [cache_len[b], cache_len[b]+S).  Returns q [B, Hq, S, D].
+
+    Replaces qwen3/modeling.rs:382-423 + update_kv_cache's slice_set (:324-327);
+    order "rope_then_norm" is Hunyuan's (hunyuan_dense/modeling.rs:541-555) and
+    "rope_only" Qwen2.5's (qwen2.rs:75-76).  `max_rows` is a host-side bound
+    on cache_len[b] + S, checked against the cache capacity."""
+    dev = _dev(qkv, cos, sin, positions, k_cache, v_cache, cache_len, q_norm_w, k_norm_w)
+    if qkv.dim() != 3:
+        raise CraneHipError(_lib.E_INVALID, "qkv must be [B, S, (Hq+2Hkv)*D]")
+    B, S, W = qkv.shape
+    D = HEAD_DIM
+    if W != (num_heads + 2 * num_kv_heads) * D:
+        raise CraneHipError(_lib.E_INVALID, f"qkv last dim {W} != (Hq+2Hkv)*{D}")
+    if k_cache.shape != v_cache.shape or k_cache.dim() != 4 or k_cache.shape[0] != B or \
+            k_cache.shape[1] != num_kv_heads or k_cache.shape[3] != D:
+        raise CraneHipError(_lib.E_INVALID, "caches must be [B, Hkv, cap, D]")
+    dt = _dtype_code(qkv)
+    for t, name in ((cos, "cos"), (sin, "sin"), (k_cache, "k_cache"), (v_cache, "v_cache"),
+                    (q_norm_w, "q_norm_w"), (k_norm_w, "k_norm_w")):
+        if t is not None and t.dtype != qkv.dtype:
+            raise CraneHipError(_lib.E_DTYPE, f"{name} dtype {t.dtype} != qkv dtype {qkv.dtype}")
+    if qkv.stride(2) != 1 or qkv.stride(0) != S * qkv.stride(1):
+        raise CraneHipError(_lib.E_INVALID, "qkv rows must be dense with a unit inner stride")
+    for t, name in ((cos, "cos"), (sin, "sin"), (k_cache, "k_cache"), (v_cache, "v_cache")):
+        _contig(t, name)
+    if cos.shape != sin.shape or cos.dim() != 2 or cos.shape[1] != D // 2:
+        raise CraneHipError(_lib.E_INVALID, "cos/sin must be [max_pos, D/2]")
+    _i32(positions, B, "positions")
+    _i32(cache_len, B, "cache_len")
+    if order not in _ORDERS:
+        raise CraneHipError(_lib.E_INVALID, f"order {order!r}")
+    q_out = torch.empty((B, num_heads, S, D), dtype=qkv.dtype, device=dev)
+    rc = _lib.lib().crane_hip_qknorm_rope_append(
+        qkv.data_ptr(), qkv.stride(1), _ptr(q_norm_w), _ptr(k_norm_w), eps, _ORDERS[order],
+        cos.data_ptr(), sin.data_ptr(), cos.stride(0), cos.shape[0], positions.data_ptr(),
+        q_out.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), k_cache.shape[2],
+        cache_len.data_ptr(), max_rows, B, S, num_heads, num_kv_heads, D, dt, _stream(dev))
+    check(rc, "qk_norm_rope_append")
+    return q_out
+
+
+# ---------------------------------------------------------------- decode op
+
+def decode_workspace_bytes(batch: int, num_heads: int, num_kv_heads: int, max_kv: int,
+                           dtype: torch.dtype = torch.bfloat16) -> int:
+    return int(_lib.lib().crane_hip_attn_decode_workspace(batch, num_heads, num_kv_heads, HEAD_DIM,
+                                                          max_kv, _DTYPES.get(dtype, 0)))
+
+
+_WORKSPACES: dict = {}
+
+
+def decode_workspace(device: torch.device, nbytes: int) -> torch.Tensor:
+    """A zero-filled per-(device, stream) workspace, grown on demand.  The decode
+    kernel leaves it zero-filled after each call, so it is reused as is."""
+    key = (device, torch.cuda.current_stream(device).cuda_stream)
+    ws = _WORKSPACES.get(key)
+    if ws is None or ws.numel() < nbytes:
+        ws = torch.zeros(max(nbytes, 256), dtype=torch.uint8, device=device)
+        _WORKSPACES[key] = ws
+    return ws
+
+
+def attention_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
+                     kv_len: torch.Tensor, max_kv: int, scale: Optional[float] = None,
+                     workspace: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Batched decode attention, one new token per sequence: q [B, Hq, D] (or
+    [B, Hq, 1, D]) over cache rows [0, kv_len[b]).  Returns [B, 1, Hq*D].
+
+    Replaces the GQA-grouped decode SDPA of qwen3/modeling.rs:432-467 and the
+    pad + mask of the batched path (:1118-1200)."""
+    dev = _dev(q, k_cache, v_cache, kv_len, workspace)
+    if q.dim() == 4:
+        if q.shape[2] != 1:
+            raise CraneHipError(_lib.E_INVALID, "decode q must hold one token per sequence")
+        q = q.reshape(q.shape[0], q.shape[1], q.shape[3])
+    if q.dim() != 3 or q.shape[2] != HEAD_DIM:
+        raise CraneHipError(_lib.E_HEAD_DIM if q.dim() == 3 else _lib.E_INVALID, "q must be [B, Hq, 128]")
+    B, Hq, D = q.shape
+    if k_cache.shape != v_cache.shape or k_cache.dim() != 4 or k_cache.shape[0] != B or k_cache.shape[3] != D:
+        raise CraneHipError(_lib.E_INVALID, "caches must be [B, Hkv, cap, D]")
+    Hkv = k_cache.shape[1]
+    for t, name in ((q, "q"), (k_cache, "k_cache"), (v_cache, "v_cache")):
+        _contig(t, name)
+        if t.dtype != q.dtype:
+            raise CraneHipError(_lib.E_DTYPE, f"{name} dtype {t.dtype} != {q.dtype}")
+    dt = _dtype_code(q)
+    _i32(kv_len, B, "kv_len")
+    scale = 1.0 / math.sqrt(D) if scale is None else float(scale)
+    need = decode_workspace_bytes(B, Hq, Hkv, max_kv, q.dtype)
+    if workspace is None:
+        workspace = decode_workspace(dev, need)
+    out = torch.empty((B, 1, Hq * D), dtype=q.dtype, device=dev)
+    rc = _lib.lib().crane_hip_attn_decode(
+        q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), k_cache.shape[2], kv_len.data_ptr(),
+        max_kv, B, Hq, Hkv, D, scale, workspace.data_ptr(), workspace.numel() * workspace.element_size(),
+        out.data_ptr(), dt, _stream(dev))
+    check(rc, "attention_decode")
+    return out
+
+
+# --------------------------------------------------------------- prefill op
+
+def attention_prefill(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
+                      start_pos: torch.Tensor, max_start: int, scale: Optional[float] = None,
+                      causal: bool = True) -> torch.Tensor:
+    """Causal GQA prefill: q [B, Hq, S, D] against cache rows [0, start_pos[b]+S).
+    Returns [B, S, Hq*D].  Replaces qwen3/modeling.rs:469-502 with the mask of
+    :866-884."""
+    dev = _dev(q, k_cache, v_cache, start_pos)
+    if q.dim() != 4:
+        raise CraneHipError(_lib.E_INVALID, "q must be [B, Hq, S, D]")
+    B, Hq, S, D = q.shape
+    if D != HEAD_DIM:
+        raise CraneHipError(_lib.E_HEAD_DIM, f"head_dim {D}")
+    if k_cache.shape != v_cache.shape or k_cache.dim() != 4 or k_cache.shape[0] != B or k_cache.shape[3] != D:
+        raise CraneHipError(_lib.E_INVALID, "caches must be [B, Hkv, cap, D]")
+    for t, name in ((q, "q"), (k_cache, "k_cache"), (v_cache, "v_cache")):
+        _contig(t, name)
+        if t.dtype != q.dtype:
+            raise CraneHipError(_lib.E_DTYPE, f"{name} dtype {t.dtype} != {q.dtype}")
+    dt = _dtype_code(q)
+    _i32(start_pos, B, "start_pos")
+    scale = 1.0 / math.sqrt(D) if scale is None else float(scale)
+    out = torch.empty((B, S, Hq * D), dtype=q.dtype, device=dev)
+    rc = _lib.lib().crane_hip_attn_prefill(
+        q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), k_cache.shape[2], start_pos.data_ptr(),
+        max_start, B, S, Hq, k_cache.shape[1], D, scale, int(bool(causal)), out.data_ptr(), dt, _stream(dev))
+    check(rc, "attention_prefill")
+    return out

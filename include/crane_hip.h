@@ -1,0 +1,144 @@
+/*
+ * crane_hip.h -- C ABI of the MI355X (gfx950) attention path for Crane.
+ *
+ * These launchers replace the candle op chain inside Crane's
+ * Attention::forward for Qwen3 / Hunyuan-dense / Qwen2.5-style models:
+ *
+ *   crane_hip_qknorm_rope_append  replaces  qwen3/modeling.rs:382-423 (qkv narrow,
+ *       head reshape/transpose, q_norm/k_norm RmsNorm, candle_nn::rotary_emb::rope)
+ *       and :313-370 (update_kv_cache slice_set), hunyuan_dense/modeling.rs:517-557
+ *       (rope then norm) and qwen25/qwen2.rs:166-183 (rope only, cache append)
+ *   crane_hip_attn_decode         replaces  qwen3/modeling.rs:432-467 (GQA-grouped
+ *       decode SDPA: q*scale, q@K^T, +mask, softmax_last_dim, @V) and the
+ *       batched-decode pad/mask of :1118-1200 (each sequence reads its own
+ *       kv_len rows, which equals right-aligned padding with -1e9 on the pad);
+ *       hunyuan_dense/modeling.rs:575-608; qwen2.rs:185-206 (repeat_kv + SDPA)
+ *   crane_hip_attn_prefill        replaces  qwen3/modeling.rs:469-502 (expand K/V,
+ *       q@K^T*scale, +causal mask of :866-884, softmax, @V, transpose to
+ *       [B,S,Hq*D]); hunyuan_dense/modeling.rs:610-645; qwen2.rs:191-211
+ *
+ * Conventions (mirroring Crane's fused_ops CustomOp1 surface,
+ * crane-core/src/fused_ops/cuda_impl.rs:43-195, where a bad shape or dtype is
+ * a `bail!` and never a crash):
+ *   - every launcher returns 0 on success or a CRANE_HIP_E_* code; argument
+ *     checks happen on the host before anything is enqueued;
+ *   - all pointers are caller-owned device memory (except where noted);
+ *     launchers never allocate and are ordered on `stream` (a hipStream_t,
+ *     NULL = the default stream); they keep no state between calls and are
+ *     re-entrant;
+ *   - dtype: CRANE_HIP_F32 or CRANE_HIP_BF16; the cos/sin tables, q, k, v, the
+ *     caches and the outputs all share it (Crane casts its tables to the model
+ *     dtype, qwen3/modeling.rs:857-864); arithmetic is f32 throughout;
+ *   - head_dim D must be 128 (every supported model family uses 128);
+ *   - KV cache layout is Crane's: [B, Hkv, cap, D], rows of D contiguous;
+ *   - q head h reads kv head h / (Hq / Hkv) (qwen3/modeling.rs:440, utils.rs:48-58).
+ */
+#ifndef CRANE_HIP_H
+#define CRANE_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define CRANE_HIP_ABI_VERSION 1
+
+enum crane_hip_dtype { CRANE_HIP_F32 = 0, CRANE_HIP_BF16 = 1 };
+
+/* Order of the per-head ops in the fused append.  Qwen3: RmsNorm then RoPE
+ * (qwen3/modeling.rs:410-423); Hunyuan: RoPE then RmsNorm
+ * (hunyuan_dense/modeling.rs:541-555); Qwen2.5: RoPE only (qwen2.rs:75-76). */
+enum crane_hip_order {
+    CRANE_HIP_NORM_THEN_ROPE = 0,
+    CRANE_HIP_ROPE_THEN_NORM = 1,
+    CRANE_HIP_ROPE_ONLY = 2
+};
+
+enum crane_hip_status {
+    CRANE_HIP_OK = 0,
+    CRANE_HIP_E_INVALID = 1,     /* a size, stride or pointer argument is invalid          */
+    CRANE_HIP_E_DTYPE = 2,       /* dtype not f32/bf16                                       */
+    CRANE_HIP_E_HEAD_DIM = 3,    /* head_dim other than 128                                  */
+    CRANE_HIP_E_GQA = 4,         /* Hq not a multiple of Hkv, or group too large             */
+    CRANE_HIP_E_CAPACITY = 5,    /* rows would land past the cache capacity                  */
+    CRANE_HIP_E_WORKSPACE = 6,   /* workspace missing or smaller than the query says         */
+    CRANE_HIP_E_LAUNCH = 7,      /* the HIP runtime rejected the launch                      */
+    CRANE_HIP_E_ALIGN = 8        /* a pointer or stride breaks the 16-byte row alignment     */
+};
+
+/* Human-readable text for a status code (static storage). */
+const char* crane_hip_strerror(int code);
+
+/* Fused per-head QK-RMSNorm + RoPE + KV-cache append.
+ *
+ * qkv       [B, S, (Hq+2*Hkv)*D] merged projection rows (Crane's qkv_proj output,
+ *           qwen3/modeling.rs:382-387), row r at qkv + r*qkv_row_stride elements
+ * q_norm_w, k_norm_w  [D] RmsNorm weights, or NULL for weight 1 (ignored for ROPE_ONLY)
+ * eps       RmsNorm epsilon (config rms_norm_eps)
+ * cos, sin  [table_rows, D/2] tables in `dtype`, row p at cos + p*cs_stride elements
+ * positions [B] int32, device: token s of sequence b uses table row positions[b]+s;
+ *           a token whose row falls outside [0, table_rows) is not written
+ * q_out     [B, Hq, S, D] rotated (and normed) queries
+ * k_cache, v_cache [B, Hkv, cache_cap, D]: token s of sequence b lands in row
+ *           cache_len[b]+s; no other row is touched
+ * cache_len [B] int32, device, the rows already valid per sequence (not updated)
+ * max_rows  host-side bound: the caller promises cache_len[b] + S <= max_rows
+ *           (<= cache_cap), which the launcher checks against cache_cap; the
+ *           kernel additionally skips any token whose row would reach cache_cap.
+ * Replaces: see the file header. */
+int crane_hip_qknorm_rope_append(const void* qkv, int64_t qkv_row_stride,
+                                 const void* q_norm_w, const void* k_norm_w, float eps,
+                                 int order, const void* cos, const void* sin, int64_t cs_stride,
+                                 int64_t table_rows, const int32_t* positions, void* q_out, void* k_cache,
+                                 void* v_cache, int64_t cache_cap, const int32_t* cache_len,
+                                 int64_t max_rows, int B, int S, int Hq, int Hkv, int D,
+                                 int dtype, void* stream);
+
+/* Bytes of workspace crane_hip_attn_decode needs for these sizes (max_kv is
+ * the largest kv_len the call may see). */
+size_t crane_hip_attn_decode_workspace(int B, int Hq, int Hkv, int D, int64_t max_kv, int dtype);
+
+/* Batched split-KV decode attention, one new token per sequence.
+ *
+ * q        [B, Hq, D] (the decode q_out of the append)
+ * k_cache, v_cache [B, Hkv, cache_cap, D]
+ * kv_len   [B] int32, device: sequence b attends rows [0, kv_len[b]) (new token
+ *          included); 1 <= kv_len[b] <= max_kv <= cache_cap.  A sequence with
+ *          kv_len[b] == 0 gets an all-zero output row.
+ * scale    softmax scale (1/sqrt(D) in every supported model)
+ * out      [B, 1, Hq*D]
+ * workspace device scratch of at least crane_hip_attn_decode_workspace(...) bytes,
+ *          16-byte aligned, zero-filled before its first use.  Every call leaves
+ *          it zero-filled again, so one workspace serves any number of
+ *          stream-ordered calls; calls that overlap in time must not share one.
+ * Replaces: qwen3/modeling.rs:432-467 and :1118-1200 (see the file header). */
+int crane_hip_attn_decode(const void* q, const void* k_cache, const void* v_cache,
+                          int64_t cache_cap, const int32_t* kv_len, int64_t max_kv, int B,
+                          int Hq, int Hkv, int D, float scale, void* workspace,
+                          size_t ws_bytes, void* out, int dtype, void* stream);
+
+/* Causal (or full) GQA prefill attention over the cache.
+ *
+ * q        [B, Hq, S, D] (the prefill q_out of the append)
+ * k_cache, v_cache [B, Hkv, cache_cap, D], holding rows [0, start_pos[b]+S)
+ * start_pos [B] int32, device: the rows cached before this chunk; query i of
+ *          sequence b sits at position start_pos[b]+i
+ * max_start host-side bound: start_pos[b] <= max_start and max_start + S <= cache_cap
+ * causal   1: key j is visible to query i iff j <= start_pos[b]+i
+ *          (qwen3/modeling.rs:866-884); 0: all start_pos[b]+S keys are visible
+ * out      [B, S, Hq*D] (qwen3/modeling.rs:497-500)
+ * Replaces: qwen3/modeling.rs:469-502 (see the file header). */
+int crane_hip_attn_prefill(const void* q, const void* k_cache, const void* v_cache,
+                           int64_t cache_cap, const int32_t* start_pos, int64_t max_start,
+                           int B, int S, int Hq, int Hkv, int D, float scale, int causal,
+                           void* out, int dtype, void* stream);
+
+/* Library and kernel-build identification, e.g. "crane_hip 1 gfx950". */
+const char* crane_hip_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* CRANE_HIP_H */

@@ -1,0 +1,74 @@
+"""Seeded inputs for the BASELINE configurations and the edge cases, shared by
+the GPU parity tests.  Host arrays are float32 holding values representable in
+the case's dtype (bf16 cases are rounded to bf16 first), so the same arrays
+feed the oracle and, converted exactly, the GPU."""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+
+D = 128
+SEED0 = 0xC3A7E000  # seed = SEED0 + config number
+
+
+def rng(seed: int) -> np.random.Generator:
+    return np.random.Generator(np.random.PCG64(seed))
+
+
+def normal(r: np.random.Generator, shape, std: float = 1.0) -> np.ndarray:
+    x = r.standard_normal(size=shape, dtype=np.float32)
+    if std != 1.0:
+        x *= np.float32(std)
+    return x
+
+
+def bf16(x: np.ndarray) -> np.ndarray:
+    """Round float32 to the nearest-even bf16 value (kept as float32)."""
+    u = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32)
+    r = ((u + np.uint32(0x7FFF) + ((u >> np.uint32(16)) & np.uint32(1))) & np.uint32(0xFFFF0000))
+    return r.view(np.float32)
+
+
+def cast(x: np.ndarray, dtype: str) -> np.ndarray:
+    return bf16(x) if dtype == "bf16" else np.ascontiguousarray(x, dtype=np.float32)
+
+
+def scale() -> float:
+    return 1.0 / math.sqrt(D)
+
+
+def decode_case(seed, B, Hq, Hkv, lens, cap=None, dtype="bf16", std=1.0, poison=True):
+    """q [B,Hq,D], K/V caches [B,Hkv,cap,D] with rows >= lens[b] set to NaN
+    (a kernel that reads past kv_len produces NaN)."""
+    r = rng(seed)
+    lens = np.asarray(lens, dtype=np.int32)
+    cap = int(cap or max(int(lens.max()), 1))
+    q = cast(normal(r, (B, Hq, D)), dtype)
+    k = cast(normal(r, (B, Hkv, cap, D), std), dtype)
+    v = cast(normal(r, (B, Hkv, cap, D), std), dtype)
+    if poison:
+        for b in range(B):
+            k[b, :, lens[b]:] = np.nan
+            v[b, :, lens[b]:] = np.nan
+    return q, k, v, lens
+
+
+def prefill_case(seed, B, S, Hq, Hkv, start, cap=None, dtype="bf16", poison=True):
+    r = rng(seed)
+    start = np.asarray(start, dtype=np.int32)
+    L = int(start.max()) + S
+    cap = int(cap or L)
+    q = cast(normal(r, (B, Hq, S, D)), dtype)
+    k = cast(normal(r, (B, Hkv, cap, D)), dtype)
+    v = cast(normal(r, (B, Hkv, cap, D)), dtype)
+    if poison:
+        for b in range(B):
+            k[b, :, start[b] + S:] = np.nan
+            v[b, :, start[b] + S:] = np.nan
+    return q, k, v, start
+
+
+def c3_lengths() -> np.ndarray:
+    """Config 3: 32 per-sequence lengths uniform in [512, 4096] (seeded)."""
+    return rng(SEED0 + 3).integers(512, 4096, size=32, endpoint=True).astype(np.int32)

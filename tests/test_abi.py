@@ -1,0 +1,147 @@
+"""C-ABI checks that need no GPU: the library loads, exports every symbol the
+header declares with the expected arity, and the host-side argument checks
+return the documented status codes before anything is enqueued (the analogue
+of the `bail!` checks in crane-core/src/fused_ops/cuda_impl.rs:61-72)."""
+import ctypes
+import os
+import re
+
+import pytest
+
+from crane_amd import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "crane_hip.h")
+
+
+def _declared():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    decls = {}
+    for m in re.finditer(r"\b(?:int|size_t|const char\s*\*)\s+(crane_hip_\w+)\s*\(([^)]*)\)\s*;", text):
+        args = [a for a in m.group(2).split(",") if a.strip() and a.strip() != "void"]
+        decls[m.group(1)] = len(args)
+    return decls
+
+
+def test_header_declares_the_path():
+    d = _declared()
+    assert set(d) == {"crane_hip_strerror", "crane_hip_version", "crane_hip_qknorm_rope_append",
+                      "crane_hip_attn_decode_workspace", "crane_hip_attn_decode", "crane_hip_attn_prefill"}
+
+
+def test_library_exports_every_declared_symbol():
+    L = _lib.lib()
+    for name, nargs in _declared().items():
+        assert hasattr(L, name), name
+        assert len(_lib.SIGNATURES[name][0]) == nargs, name
+
+
+def test_strerror_and_version():
+    assert _lib.version().startswith("crane_hip 1 gfx950")
+    for code in range(0, 9):
+        assert _lib.strerror(code)
+    assert "capacity" in _lib.strerror(_lib.E_CAPACITY)
+    assert _lib.strerror(99) == "unknown crane_hip status"
+
+
+def _decode(**kw):
+    a = dict(q=16, k=16, v=16, cap=4096, kv_len=16, max_kv=4096, B=1, Hq=32, Hkv=8, D=128, scale=0.088,
+             ws=16, ws_bytes=1 << 30, out=16, dtype=1, stream=None)
+    a.update(kw)
+    return _lib.lib().crane_hip_attn_decode(a["q"], a["k"], a["v"], a["cap"], a["kv_len"], a["max_kv"], a["B"],
+                                            a["Hq"], a["Hkv"], a["D"], a["scale"], a["ws"], a["ws_bytes"],
+                                            a["out"], a["dtype"], a["stream"])
+
+
+@pytest.mark.parametrize("kw,code", [
+    (dict(dtype=2), _lib.E_DTYPE),
+    (dict(D=64), _lib.E_HEAD_DIM),
+    (dict(Hq=30), _lib.E_GQA),
+    (dict(max_kv=5000), _lib.E_CAPACITY),
+    (dict(max_kv=0), _lib.E_INVALID),
+    (dict(scale=0.0), _lib.E_INVALID),
+    (dict(q=None), _lib.E_INVALID),
+    (dict(q=8), _lib.E_ALIGN),
+    (dict(ws_bytes=100), _lib.E_WORKSPACE),
+    (dict(ws=None), _lib.E_WORKSPACE),
+    (dict(B=0), _lib.OK),                 # empty batch: nothing to do
+])
+def test_decode_argument_checks(kw, code):
+    assert _decode(**kw) == code
+
+
+def test_decode_workspace_size():
+    L = _lib.lib()
+    ns = (4096 + 255) // 256
+    o = 32 * 32 * ns * 128 * 4
+    ml = 32 * 32 * ns * 2 * 4
+    cnt = 32 * 32 * 4                      # one completion counter per (sequence, head group), padded
+    up = lambda x: (x + 255) // 256 * 256
+    assert L.crane_hip_attn_decode_workspace(32, 32, 8, 128, 4096, 1) == up(o) + up(ml) + up(cnt)
+    assert L.crane_hip_attn_decode_workspace(32, 32, 8, 64, 4096, 1) == 0
+    assert L.crane_hip_attn_decode_workspace(0, 32, 8, 128, 4096, 1) == 0
+
+
+def _prefill(**kw):
+    a = dict(q=16, k=16, v=16, cap=4096, start=16, max_start=0, B=1, S=2048, Hq=16, Hkv=8, D=128, scale=0.088,
+             causal=1, out=16, dtype=1, stream=None)
+    a.update(kw)
+    return _lib.lib().crane_hip_attn_prefill(a["q"], a["k"], a["v"], a["cap"], a["start"], a["max_start"], a["B"],
+                                             a["S"], a["Hq"], a["Hkv"], a["D"], a["scale"], a["causal"], a["out"],
+                                             a["dtype"], a["stream"])
+
+
+@pytest.mark.parametrize("kw,code", [
+    (dict(dtype=5), _lib.E_DTYPE),
+    (dict(D=256), _lib.E_HEAD_DIM),
+    (dict(Hkv=3), _lib.E_GQA),
+    (dict(max_start=2049), _lib.E_CAPACITY),
+    (dict(S=4097), _lib.E_CAPACITY),
+    (dict(max_start=-1), _lib.E_INVALID),
+    (dict(out=None), _lib.E_INVALID),
+    (dict(k=24), _lib.E_ALIGN),
+    (dict(S=0), _lib.OK),
+])
+def test_prefill_argument_checks(kw, code):
+    assert _prefill(**kw) == code
+
+
+def _append(**kw):
+    a = dict(qkv=16, stride=4096, qw=None, kw=None, eps=1e-6, order=0, cos=16, sin=16, cs_stride=64,
+             rows=40960, pos=16, q_out=16, kc=16, vc=16, cap=4096, clen=16, max_rows=4096, B=1, S=2048,
+             Hq=16, Hkv=8, D=128, dtype=1, stream=None)
+    a.update(kw)
+    return _lib.lib().crane_hip_qknorm_rope_append(
+        a["qkv"], a["stride"], a["qw"], a["kw"], a["eps"], a["order"], a["cos"], a["sin"], a["cs_stride"],
+        a["rows"], a["pos"], a["q_out"], a["kc"], a["vc"], a["cap"], a["clen"], a["max_rows"], a["B"], a["S"],
+        a["Hq"], a["Hkv"], a["D"], a["dtype"], a["stream"])
+
+
+@pytest.mark.parametrize("kw,code", [
+    (dict(dtype=3), _lib.E_DTYPE),
+    (dict(D=96), _lib.E_HEAD_DIM),
+    (dict(Hkv=5), _lib.E_GQA),
+    (dict(order=3), _lib.E_INVALID),
+    (dict(max_rows=4097), _lib.E_CAPACITY),
+    (dict(S=5000, max_rows=4096), _lib.E_CAPACITY),
+    (dict(stride=4000), _lib.E_INVALID),
+    (dict(stride=4098), _lib.E_ALIGN),
+    (dict(cs_stride=32), _lib.E_INVALID),
+    (dict(rows=0), _lib.E_INVALID),
+    (dict(cos=None), _lib.E_INVALID),
+    (dict(qw=20), _lib.E_ALIGN),
+    (dict(eps=-1.0), _lib.E_INVALID),
+    (dict(S=0), _lib.OK),
+])
+def test_append_argument_checks(kw, code):
+    assert _append(**kw) == code
+
+
+def test_ops_reject_cpu_tensors():
+    import torch
+    from crane_amd import ops
+    q = torch.zeros(1, 8, 128, dtype=torch.bfloat16)
+    k = torch.zeros(1, 2, 16, 128, dtype=torch.bfloat16)
+    with pytest.raises(_lib.CraneHipError, match="GPU only"):
+        ops.attention_decode(q, k, k, torch.ones(1, dtype=torch.int32), 16)

@@ -1,0 +1,217 @@
+"""GPU parity: every kernel through the C ABI against the CPU oracle on the
+same seeded inputs, at the BASELINE configurations (full size where the
+oracle finishes in seconds, sampled rows otherwise) and at the edge cases.
+Bars: f32 max-abs <= 1e-4; bf16 max-abs <= 2e-2 and mean-rel <= 1e-2.
+Cache rows the kernels must not read are NaN, so an out-of-range read fails."""
+import math
+import sys
+import zlib
+
+import numpy as np
+import pytest
+import torch
+
+from tests import cases
+from tests.cases import D
+from tests.tolerance import assert_close
+
+pytestmark = pytest.mark.gpu
+
+
+def dev_t(x, dtype, dev):
+    t = torch.from_numpy(np.ascontiguousarray(x))
+    if dtype == "bf16":
+        t = t.to(torch.bfloat16)
+    return t.to(dev).contiguous()
+
+
+def host(t):
+    return t.float().cpu().numpy()
+
+
+def i32(x, dev):
+    return torch.as_tensor(np.asarray(x, dtype=np.int32), device=dev).contiguous()
+
+
+def note(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+# ------------------------------------------------------------------ decode
+
+DECODE_CASES = [
+    # name, B, Hq, Hkv, lens, dtype, std
+    ("c1_qwen3_0.6b_f32", 1, 16, 8, [1025], "f32", 1.0),
+    ("c3_qwen3_8b_bf16", 32, 32, 8, None, "bf16", 1.0),
+    ("ragged_edges_bf16", 6, 8, 2, [1, 255, 256, 257, 511, 1000], "bf16", 1.0),
+    ("ragged_edges_f32", 5, 8, 2, [1, 2, 256, 257, 700], "f32", 1.0),
+    ("mha_nrep1_bf16", 3, 4, 4, [17, 300, 64], "bf16", 1.0),
+    ("qwen25_7b_gqa7_bf16", 4, 28, 4, [100, 1500, 4096, 33], "bf16", 1.0),
+    ("gqa16_bf16", 2, 32, 2, [513, 2000], "bf16", 1.0),
+    ("gqa3_f32", 2, 6, 2, [40, 900], "f32", 1.0),
+]
+
+
+@pytest.mark.parametrize("name,B,Hq,Hkv,lens,dtype,std", DECODE_CASES, ids=[c[0] for c in DECODE_CASES])
+def test_decode_parity(gpu, orc, name, B, Hq, Hkv, lens, dtype, std):
+    from crane_amd import ops
+    if lens is None:
+        lens = cases.c3_lengths()
+    note(f"decode {name}: B={B} Hq={Hq} Hkv={Hkv} dtype={dtype} max_len={max(lens)}")
+    q, k, v, lens = cases.decode_case(cases.SEED0 + zlib.crc32(name.encode()) % 1000, B, Hq, Hkv, lens, dtype=dtype, std=std)
+    cap = k.shape[2]
+    out = ops.attention_decode(dev_t(q, dtype, gpu), dev_t(k, dtype, gpu), dev_t(v, dtype, gpu), i32(lens, gpu),
+                               int(lens.max()), cases.scale())
+    torch.cuda.synchronize()
+    ref = orc.attn_decode(q, k, v, lens, cases.scale(), dtype)
+    assert_close(host(out).reshape(B, Hq * D), ref, dtype, name)
+    assert cap == int(lens.max())
+
+
+def test_decode_c5_long_context(gpu, orc):
+    """Config 5 (Qwen2.5-72B shape, 32768-token cache, K/V ~ N(0, 0.5)) on 2
+    of the 8 sequences, so the oracle stays within seconds."""
+    from crane_amd import ops
+    B, Hq, Hkv, L = 2, 64, 8, 32768
+    note("decode c5: B=2 Hq=64 Hkv=8 L=32768 bf16")
+    q, k, v, lens = cases.decode_case(cases.SEED0 + 5, B, Hq, Hkv, [L, L], dtype="bf16",
+                                      std=math.sqrt(0.5), poison=False)
+    out = ops.attention_decode(dev_t(q, "bf16", gpu), dev_t(k, "bf16", gpu), dev_t(v, "bf16", gpu),
+                               i32(lens, gpu), L)
+    ref = orc.attn_decode(q, k, v, lens, cases.scale(), "bf16", orc.DECODE_STANDARD)
+    assert_close(host(out).reshape(B, Hq * D), ref, "bf16", "c5")
+
+
+def test_decode_zero_length_and_cap_larger_than_len(gpu, orc):
+    from crane_amd import ops
+    q, k, v, lens = cases.decode_case(77, 3, 8, 2, [0, 5, 300], cap=1024, dtype="bf16")
+    out = host(ops.attention_decode(dev_t(q, "bf16", gpu), dev_t(k, "bf16", gpu), dev_t(v, "bf16", gpu),
+                                    i32(lens, gpu), 300)).reshape(3, 8 * D)
+    assert np.all(out[0] == 0.0)
+    ref = orc.attn_decode(q[1:], k[1:], v[1:], lens[1:], cases.scale(), "bf16")
+    assert_close(out[1:], ref, "bf16", "zero-length batch")
+
+
+def test_decode_kv_len_clamped_to_max_kv(gpu, orc):
+    """A kv_len above the host's max_kv is clamped, never read past."""
+    from crane_amd import ops
+    q, k, v, lens = cases.decode_case(78, 2, 8, 2, [100, 100], cap=100, dtype="bf16")
+    out = host(ops.attention_decode(dev_t(q, "bf16", gpu), dev_t(k, "bf16", gpu), dev_t(v, "bf16", gpu),
+                                    i32([1000, 50], gpu), 100)).reshape(2, 8 * D)
+    ref = orc.attn_decode(q, k, v, np.array([100, 50], np.int32), cases.scale(), "bf16")
+    assert_close(out, ref, "bf16", "clamp")
+
+
+def test_decode_properties_full_c3(gpu):
+    """Size-independent properties at config 3's full size: V = 1 gives 1
+    (probabilities sum to one); permuting cache rows leaves the output unchanged."""
+    from crane_amd import ops
+    lens = cases.c3_lengths()
+    B, Hq, Hkv = 32, 32, 8
+    q, k, v, lens = cases.decode_case(cases.SEED0 + 31, B, Hq, Hkv, lens, dtype="bf16", poison=False)
+    qd, kd = dev_t(q, "bf16", gpu), dev_t(k, "bf16", gpu)
+    ones = torch.ones_like(kd)
+    out = host(ops.attention_decode(qd, kd, ones, i32(lens, gpu), int(lens.max())))
+    assert np.all(out == 1.0)
+    vd = dev_t(v, "bf16", gpu)
+    base = host(ops.attention_decode(qd, kd, vd, i32(lens, gpu), int(lens.max())))
+    kp, vp = kd.clone(), vd.clone()
+    g = torch.Generator().manual_seed(5)
+    for b in range(B):
+        perm = torch.randperm(int(lens[b]), generator=g).to(gpu)
+        kp[b, :, :lens[b]] = kd[b, :, perm]
+        vp[b, :, :lens[b]] = vd[b, :, perm]
+    permuted = host(ops.attention_decode(qd, kp, vp, i32(lens, gpu), int(lens.max())))
+    assert np.max(np.abs(permuted - base)) <= 2 ** -7 * max(1.0, np.abs(base).max())
+
+
+# ------------------------------------------------------------------ append
+
+APPEND_CASES = [
+    # name, B, S, Hq, Hkv, cache_len, positions, cap, order, dtype
+    ("c2_prefill_append_bf16", 1, 2048, 16, 8, [0], [0], 4096, 0, "bf16"),
+    ("c1_decode_append_f32", 1, 1, 16, 8, [1024], [1024], 1025, 0, "f32"),
+    ("batched_decode_append_bf16", 32, 1, 32, 8, list(range(500, 532)), list(range(700, 732)), 600, 0, "bf16"),
+    ("hunyuan_order_bf16", 2, 33, 8, 2, [0, 5], [0, 5], 64, 1, "bf16"),
+    ("qwen25_rope_only_bf16", 2, 70, 28, 4, [3, 0], [3, 0], 80, 2, "bf16"),
+    ("hunyuan_order_f32", 2, 9, 4, 2, [1, 2], [1, 2], 16, 1, "f32"),
+    ("qwen3_prefill_f32", 1, 40, 16, 8, [0], [0], 64, 0, "f32"),
+]
+
+
+@pytest.mark.parametrize("name,B,S,Hq,Hkv,clen,posn,cap,order,dtype", APPEND_CASES, ids=[c[0] for c in APPEND_CASES])
+def test_append_parity(gpu, orc, name, B, S, Hq, Hkv, clen, posn, cap, order, dtype):
+    from crane_amd import ops
+    note(f"append {name}: B={B} S={S} Hq={Hq} Hkv={Hkv} order={order} dtype={dtype}")
+    r = cases.rng(cases.SEED0 + 200 + len(name))
+    qkv = cases.cast(cases.normal(r, (B, S, (Hq + 2 * Hkv) * D)), dtype)
+    qw = cases.cast(1 + 0.1 * cases.normal(r, (D,)), dtype) if order != 2 else None
+    kw = cases.cast(1 + 0.1 * cases.normal(r, (D,)), dtype) if order != 2 else None
+    cos, sin = orc.rope_tables(D, 1e6, 4096)
+    cos, sin = cases.cast(cos, dtype), cases.cast(sin, dtype)
+    canary = np.float32(3.0)
+    kc = np.full((B, Hkv, cap, D), canary, np.float32)
+    vc = np.full((B, Hkv, cap, D), canary, np.float32)
+    kd, vd = dev_t(kc, dtype, gpu), dev_t(vc, dtype, gpu)
+    q = ops.qk_norm_rope_append(dev_t(qkv, dtype, gpu), dev_t(cos, dtype, gpu), dev_t(sin, dtype, gpu),
+                                i32(posn, gpu), kd, vd, i32(clen, gpu), max(clen) + S, Hq, Hkv,
+                                None if qw is None else dev_t(qw, dtype, gpu),
+                                None if kw is None else dev_t(kw, dtype, gpu), 1e-6,
+                                ["norm_then_rope", "rope_then_norm", "rope_only"][order])
+    torch.cuda.synchronize()
+    q_ref = orc.qk_norm_rope_append(qkv, Hq, Hkv, cos, sin, np.array(posn, np.int32), kc, vc,
+                                    np.array(clen, np.int32), qw, kw, 1e-6, order, dtype)
+    assert_close(host(q), q_ref, dtype, name + " q")
+    kg, vg = host(kd), host(vd)
+    assert np.array_equal(vg, vc), "value rows are a copy"
+    assert_close(kg, kc, dtype, name + " k")
+    untouched = np.ones((B, cap), bool)
+    for b in range(B):
+        untouched[b, clen[b]:clen[b] + S] = False
+    assert np.all(kg.transpose(0, 2, 1, 3)[untouched] == canary)
+
+
+# ----------------------------------------------------------------- prefill
+
+PREFILL_CASES = [
+    # name, B, S, Hq, Hkv, start, causal, dtype, rows (sampled) or None
+    ("c2_qwen3_0.6b_bf16", 1, 2048, 16, 8, [0], True, "bf16", [(0, 128), (1000, 1100), (1920, 2048)]),
+    ("c4_qwen25_7b_bf16", 8, 4096, 28, 4, [0] * 8, True, "bf16", [(0, 64), (2011, 2075), (4032, 4096)]),
+    ("ragged_S_bf16", 2, 200, 8, 2, [0, 0], True, "bf16", None),
+    ("continuation_bf16", 3, 77, 6, 2, [0, 130, 1000], True, "bf16", None),
+    ("noncausal_bf16", 2, 96, 8, 4, [0, 40], False, "bf16", None),
+    ("mha_bf16", 1, 300, 4, 4, [0], True, "bf16", None),
+    ("tiny_S1_bf16", 2, 1, 8, 2, [0, 63], True, "bf16", None),
+    ("f32_small", 2, 50, 4, 2, [0, 17], True, "f32", None),
+]
+
+
+@pytest.mark.parametrize("name,B,S,Hq,Hkv,start,causal,dtype,rows", PREFILL_CASES, ids=[c[0] for c in PREFILL_CASES])
+def test_prefill_parity(gpu, orc, name, B, S, Hq, Hkv, start, causal, dtype, rows):
+    from crane_amd import ops
+    note(f"prefill {name}: B={B} S={S} Hq={Hq} Hkv={Hkv} start={start} causal={causal} dtype={dtype}")
+    q, k, v, st = cases.prefill_case(cases.SEED0 + 300 + len(name), B, S, Hq, Hkv, start, dtype=dtype)
+    out = host(ops.attention_prefill(dev_t(q, dtype, gpu), dev_t(k, dtype, gpu), dev_t(v, dtype, gpu),
+                                     i32(st, gpu), int(st.max()), cases.scale(), causal)).reshape(B, S, Hq, D)
+    assert np.all(np.isfinite(out))
+    if rows is None:
+        ref = orc.attn_prefill(q, k, v, st, cases.scale(), causal, dtype).reshape(B, S, Hq, D)
+        assert_close(out, ref, dtype, name)
+    else:
+        bsel = [0, B - 1] if B > 1 else [0]
+        for b in bsel:
+            for (r0, r1) in rows:
+                ref = orc.attn_prefill(q[b:b + 1], k[b:b + 1], v[b:b + 1], st[b:b + 1], cases.scale(), causal, dtype,
+                                       rows=(r0, r1)).reshape(1, S, Hq, D)
+                assert_close(out[b, r0:r1], ref[0, r0:r1], dtype, f"{name} b={b} rows {r0}:{r1}")
+
+
+def test_prefill_last_row_equals_decode(gpu):
+    """The last prefill row equals a decode of the same query over the same rows."""
+    from crane_amd import ops
+    q, k, v, st = cases.prefill_case(91, 2, 333, 16, 8, [0, 0], dtype="bf16", poison=False)
+    qd, kd, vd = dev_t(q, "bf16", gpu), dev_t(k, "bf16", gpu), dev_t(v, "bf16", gpu)
+    pre = host(ops.attention_prefill(qd, kd, vd, i32(st, gpu), 0))
+    dec = host(ops.attention_decode(qd[:, :, -1].contiguous(), kd, vd, i32([333, 333], gpu), 333))
+    assert np.max(np.abs(pre[:, -1] - dec[:, 0])) <= 2e-2
