@@ -11,8 +11,9 @@
 // Work item = one head row (128 elements) of one token: Hq query rows, Hkv key
 // rows and Hkv value rows per token.  16 lanes own an item; lane l holds dims
 // [4l, 4l+4) and their rotate-half partners [64+4l, 64+4l+4), so the rotation
-// is lane-local and the RMS sum is a 16-lane butterfly.  Norm and rotation run
-// in f32 and each output element is rounded to the storage type once.  Every
+// is lane-local and the RMS sum is a 16-lane butterfly.  The arithmetic is f32
+// with the result of every candle op rounded to the storage type, as Crane's
+// candle op chain rounds it (the kernel is HBM-bound, so this is free).  Every
 // cache row is written exactly once; q lands in [B,Hq,S,D] for the attention
 // kernels.  HBM traffic per token: (Hq+2Hkv)*D elements read, the same written.
 #include "common.h"
@@ -30,13 +31,20 @@ __device__ __forceinline__ float group16_sum(float v) {
     return v;
 }
 
+// candle_nn RmsNorm over the 128 dims held by 16 lanes.  `contiguous` selects
+// candle's fused ops::rms_norm (m = sqrt(mean(x^2)+eps) converted to T, then
+// x / m * w in T) or the LayerNorm fallback used for a non-contiguous input
+// (x / sqrt(mean(x^2)+eps) in f32, converted to T, then * w in T).  The sum of
+// squares accumulates in f32.
 template <typename T>
-__device__ __forceinline__ void rms_norm16(float (&x1)[4], float (&x2)[4], const T* w, int l, float eps) {
+__device__ __forceinline__ void rms_norm16(float (&x1)[4], float (&x2)[4], const T* w, int l, float eps,
+                                           bool contiguous) {
     float ss = 0.f;
 #pragma unroll
     for (int i = 0; i < 4; ++i) ss += x1[i] * x1[i] + x2[i] * x2[i];
     ss = group16_sum(ss);
-    const float inv = 1.0f / sqrtf(ss * (1.0f / kHeadDim) + eps);
+    float m = sqrtf(ss * (1.0f / kHeadDim) + eps);
+    if (contiguous) m = rt<T>(m);
     float w1[4] = {1.f, 1.f, 1.f, 1.f}, w2[4] = {1.f, 1.f, 1.f, 1.f};
     if (w) {
         load4(w + 4 * l, w1);
@@ -44,17 +52,20 @@ __device__ __forceinline__ void rms_norm16(float (&x1)[4], float (&x2)[4], const
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        x1[i] = x1[i] * inv * w1[i];
-        x2[i] = x2[i] * inv * w2[i];
+        x1[i] = rt<T>(rt<T>(x1[i] / m) * w1[i]);
+        x2[i] = rt<T>(rt<T>(x2[i] / m) * w2[i]);
     }
 }
 
+// candle_nn::rotary_emb::rope (rotate-half): every product and sum rounded in T.
+template <typename T>
 __device__ __forceinline__ void rope4(float (&x1)[4], float (&x2)[4], const float (&c)[4], const float (&s)[4]) {
+#pragma clang fp contract(off)
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const float a = x1[i], b = x2[i];
-        x1[i] = a * c[i] - b * s[i];
-        x2[i] = a * s[i] + b * c[i];
+        x1[i] = rt<T>(rt<T>(a * c[i]) - rt<T>(b * s[i]));
+        x2[i] = rt<T>(rt<T>(a * s[i]) + rt<T>(b * c[i]));
     }
 }
 
@@ -103,9 +114,11 @@ __global__ __launch_bounds__(256) void qknorm_rope_append_kernel(
     load4(cos_t + p * cs_stride + 4 * l, c);
     load4(sin_t + p * cs_stride + 4 * l, sn);
 
-    if (order == CRANE_HIP_NORM_THEN_ROPE) rms_norm16(x1, x2, w, l, eps);
-    rope4(x1, x2, c, sn);
-    if (order == CRANE_HIP_ROPE_THEN_NORM) rms_norm16(x1, x2, w, l, eps);
+    // Qwen3 norms the transposed [B,H,S,D] view, contiguous only when S == 1;
+    // Hunyuan norms the contiguous rope output.
+    if (order == CRANE_HIP_NORM_THEN_ROPE) rms_norm16(x1, x2, w, l, eps, S == 1);
+    rope4<T>(x1, x2, c, sn);
+    if (order == CRANE_HIP_ROPE_THEN_NORM) rms_norm16(x1, x2, w, l, eps, true);
 
     store4(dst + 4 * l, x1);
     store4(dst + 64 + 4 * l, x2);

@@ -74,6 +74,12 @@ __device__ __forceinline__ void load8(const bf16_t* p, float (&v)[8]) {
     v[4] = bf16_lo(t.z); v[5] = bf16_hi(t.z); v[6] = bf16_lo(t.w); v[7] = bf16_hi(t.w);
 }
 
+// Rounding to the storage type after a candle op: identity for f32,
+// round-to-nearest-even bf16 for bf16 (half::bf16 arithmetic rounds every op).
+template <typename T> __device__ __forceinline__ float rt(float x);
+template <> __device__ __forceinline__ float rt<float>(float x) { return x; }
+template <> __device__ __forceinline__ float rt<bf16_t>(float x) { return bf16_to_f32(f32_to_bf16(x)); }
+
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
 constexpr float kLog2e = 1.4426950408889634f;

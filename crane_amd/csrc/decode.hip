@@ -7,27 +7,58 @@
 // sequence b reads exactly its own kv_len[b] rows, which gives the same
 // softmax as padding with masked columns (exp(-1e9 - m) == 0 in f32).
 //
-// One kernel (decode_split_kernel): one workgroup per (chunk of kChunk keys,
-// kv head, sequence).  The G query heads that share the kv head are processed together,
-// so every K/V row is read from HBM once for the whole GQA group.  A row is
-// read by 16 lanes with one 16-byte load each (bf16: 8 dims per lane), and a
-// wave covers 4 rows per load instruction.  Scores go to LDS, the chunk's
-// softmax statistics (max m, sum l, in the log2 domain) are computed once per
-// (head, key), and P@V accumulates in f32.  A sequence that fits one chunk is
-// normalised and written directly.  Otherwise each chunk writes its
-// unnormalised f32 output and (m, l) to the workspace and bumps a per-(sequence,
-// head group) counter; the chunk that arrives last combines all partials with
-// the log-sum-exp rule, writes the normalised rows and re-arms the counter, so
-// no second launch is needed.  The counters must be zero before the first
-// call on a workspace and are zero again after every call.
+// Kernel 1 (decode_chunk_kernel): one workgroup (4 waves) per (chunk of 256
+// keys, kv head, sequence).  The G query heads sharing the kv head are done
+// together, so each K/V row is read from HBM once for the whole GQA group, and
+// no MFMA is used: the path is HBM-bound.
+//   A. scores: 16 lanes read one K row with one 16-byte load each (a wave load
+//      instruction covers 4 consecutive rows, 1 KiB); each lane does the dot
+//      product of its 8 dims with v_dot2_f32_bf16 for all G heads, and a
+//      4-step DPP butterfly inside the 16-lane row completes it.
+//   B. the chunk's softmax statistics per head (max m and sum l of the
+//      bf16-rounded exp2(s - m), log2 domain), computed once per (head, key);
+//      probabilities go to LDS as packed bf16 pairs of consecutive keys.
+//   C. P @ V: 16 lanes read a V row; two consecutive rows are interleaved
+//      with v_perm so v_dot2_f32_bf16 takes (p_j, p_j+1) x (v_j, v_j+1) per
+//      dim.  The 4 row groups of a wave are summed with lane permutes and
+//      the 4 waves through LDS.
+// A sequence that fits one chunk is normalised and written directly; longer
+// ones leave their unnormalised f32 partial and (m, l) in the workspace.
+// Kernel 2 (decode_merge_kernel): the log-sum-exp merge of those partials.
+//
+// Crane's grouped decode pre-scales q in the model dtype (candle affine with
+// the scale converted to T, qwen3/modeling.rs:440-441) and its q@K^T output is
+// a T tensor; both roundings are reproduced so the scores match candle's.
+#include <type_traits>
+
 #include "common.h"
 
 namespace crane {
 namespace {
 
-constexpr int kChunk = 256;     // keys per workgroup in pass 1
+constexpr int kChunk = 256;     // keys per workgroup
 constexpr int kThreads = 256;   // 4 waves
 constexpr int kMaxGroup = 8;    // q heads handled per workgroup
+
+template <int CTRL>
+__device__ __forceinline__ float dpp(float x) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, 0xf, 0xf, false));
+}
+
+// Sum over the 16 lanes of a DPP row; every lane gets the total.
+__device__ __forceinline__ float row16_sum(float x) {
+    x += dpp<0xB1>(x);   // quad_perm [1,0,3,2]
+    x += dpp<0x4E>(x);   // quad_perm [2,3,0,1]
+    x += dpp<0x124>(x);  // row_ror:4
+    x += dpp<0x128>(x);  // row_ror:8
+    return x;
+}
+
+// Sum over the 4 rows (16-lane groups) of the wave; every lane gets the total.
+__device__ __forceinline__ float rows4_sum(float x) {
+    x += __shfl_xor(x, 16);
+    return x + __shfl_xor(x, 32);
+}
 
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
@@ -40,14 +71,35 @@ __device__ __forceinline__ float wave_sum(float v) {
     return v;
 }
 
+__device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_v, a), __builtin_bit_cast(bf16x2_v, b), c, false);
+}
+
+// Storage per lane of one K/V row slice (8 dims).
+template <typename T> struct Row8;
+template <> struct Row8<bf16_t> { uint4 w; };
+template <> struct Row8<float> { float4 a, b; };
+
+template <typename T>
+__device__ __forceinline__ Row8<T> load_row8(const T* p, bool valid) {
+    Row8<T> r;
+    if constexpr (std::is_same<T, bf16_t>::value) {
+        r.w = valid ? *reinterpret_cast<const uint4*>(p) : make_uint4(0, 0, 0, 0);
+    } else {
+        r.a = valid ? *reinterpret_cast<const float4*>(p) : make_float4(0, 0, 0, 0);
+        r.b = valid ? *reinterpret_cast<const float4*>(p + 4) : make_float4(0, 0, 0, 0);
+    }
+    return r;
+}
+
 // grid: (nsplit, Hkv * (n_rep / G), B).  ws_o: [B, Hq, nsplit, D] f32;
-// ws_ml: [B, Hq, nsplit, 2] f32 (max, sum) in the log2 domain;
-// counters: [B, gridDim.y] int32, zero between calls.
+// ws_ml: [B, Hq, nsplit, 2] f32 (max, sum) in the log2 domain.
 template <typename T, int G>
-__global__ __launch_bounds__(kThreads) void decode_split_kernel(
+__global__ __launch_bounds__(kThreads) void decode_chunk_kernel(
     const T* __restrict__ q, const T* __restrict__ kc, const T* __restrict__ vc, int64_t cap,
-    const int32_t* __restrict__ kv_len, int max_kv, int Hq, int Hkv, int n_rep, float scale_log2, int nsplit,
-    float* __restrict__ ws_o, float* __restrict__ ws_ml, int* __restrict__ counters, T* __restrict__ out) {
+    const int32_t* __restrict__ kv_len, int max_kv, int Hq, int Hkv, int n_rep, float scale, int nsplit,
+    float* __restrict__ ws_o, float* __restrict__ ws_ml, T* __restrict__ out) {
+    constexpr bool kBf16 = std::is_same<T, bf16_t>::value;
     const int c = blockIdx.x;
     const int sub_per_kv = n_rep / G;
     const int kvh = blockIdx.y / sub_per_kv;
@@ -63,61 +115,103 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(
         return;
     }
     const int n = min(kChunk, L - j0);
-
     const int lane = tid & 63, wave = tid >> 6, grp = lane >> 4, l16 = lane & 15;
 
-    __shared__ float s_lds[kChunk][G];
-    __shared__ float red[4][G][kHeadDim];
+    __shared__ float s_lds[G][kChunk];
+    __shared__ uint32_t p_lds[kBf16 ? kChunk / 2 * G : 1];   // bf16 pairs (key 2m, 2m+1) per head
+    __shared__ float pf_lds[kBf16 ? 1 : kChunk * G];          // f32 probabilities
+    __shared__ __attribute__((aligned(16))) float red[4][G][kHeadDim];
     __shared__ float ml[G][2];
 
-    float qf[G][8];
+    // q_g = q * scale in T, for this lane's 8 dims of every head.
+    const float scale_t = rt<T>(scale);
+    uint32_t qp[G][4];
+    float qf[kBf16 ? 1 : G][8];
 #pragma unroll
     for (int h = 0; h < G; ++h) {
-        load8(q + ((int64_t)b * Hq + h0 + h) * kHeadDim + 8 * l16, qf[h]);
+        float x[8];
+        load8(q + ((int64_t)b * Hq + h0 + h) * kHeadDim + 8 * l16, x);
+        if constexpr (kBf16) {
 #pragma unroll
-        for (int d = 0; d < 8; ++d) qf[h][d] *= scale_log2;
+            for (int i = 0; i < 4; ++i) qp[h][i] = pack_bf16x2(x[2 * i] * scale_t, x[2 * i + 1] * scale_t);
+        } else {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) qf[h][i] = x[i] * scale_t;
+        }
     }
     const int64_t base = (((int64_t)b * Hkv + kvh) * cap + j0) * kHeadDim + 8 * l16;
     const T* K = kc + base;
     const T* V = vc + base;
 
-    // Phase A: scores (log2 domain) of this chunk.
-    for (int it = 0; it < kChunk / 16; ++it) {
-        const int j = it * 16 + wave * 4 + grp;
-        if (j < n) {  // uniform within a 16-lane group
-            float kf[8];
-            load8(K + (int64_t)j * kHeadDim, kf);
+    // ---- A: raw scores q_g . k for the chunk; wave w owns keys [64w, 64w+64)
+#pragma unroll
+    for (int half = 0; half < 2; ++half) {
+        Row8<T> kr[8];
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+            const int j = wave * 64 + (half * 8 + t) * 4 + grp;
+            kr[t] = load_row8(K + (int64_t)j * kHeadDim, j < n);
+        }
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+            const int j = wave * 64 + (half * 8 + t) * 4 + grp;
             float acc[G];
 #pragma unroll
             for (int h = 0; h < G; ++h) {
-                float a = 0.f;
+                if constexpr (kBf16) {
+                    float a = dot2(qp[h][0], kr[t].w.x, 0.f);
+                    a = dot2(qp[h][1], kr[t].w.y, a);
+                    a = dot2(qp[h][2], kr[t].w.z, a);
+                    acc[h] = dot2(qp[h][3], kr[t].w.w, a);
+                } else {
+                    const float* kf = reinterpret_cast<const float*>(&kr[t]);
+                    float a = 0.f;
 #pragma unroll
-                for (int d = 0; d < 8; ++d) a += qf[h][d] * kf[d];
-                acc[h] = a;
+                    for (int i = 0; i < 8; ++i) a += qf[h][i] * kf[i];
+                    acc[h] = a;
+                }
+                acc[h] = row16_sum(acc[h]);
             }
+            float mine = acc[0];
 #pragma unroll
-            for (int h = 0; h < G; ++h) {
-                acc[h] += __shfl_xor(acc[h], 1, 16);
-                acc[h] += __shfl_xor(acc[h], 2, 16);
-                acc[h] += __shfl_xor(acc[h], 4, 16);
-                acc[h] += __shfl_xor(acc[h], 8, 16);
-            }
-#pragma unroll
-            for (int h = 0; h < G; ++h)
-                if (l16 == h) s_lds[j][h] = acc[h];
+            for (int h = 1; h < G; ++h) mine = l16 == h ? acc[h] : mine;
+            if (l16 < G && j < n) s_lds[l16][j] = mine;
         }
+    }
+
+    // Prefetch this lane's V rows for C while B runs: pairs m = 32w + 4t + grp.
+    Row8<T> vr[8][2];
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+        const int m = wave * 32 + 4 * t + grp;
+#pragma unroll
+        for (int r = 0; r < 2; ++r) vr[t][r] = load_row8(V + (int64_t)(2 * m + r) * kHeadDim, 2 * m + r < n);
     }
     __syncthreads();
 
-    // Phase B: per-head chunk max and exp-sum; scores become probabilities.
+    // ---- B: per-head chunk max and sum (log2 domain); probabilities to LDS
     for (int h = wave; h < G; h += 4) {
+        float sv[kChunk / 64];
         float m = -INFINITY;
-        for (int j = lane; j < n; j += 64) m = fmaxf(m, s_lds[j][h]);
+#pragma unroll
+        for (int i = 0; i < kChunk / 64; ++i) {
+            const int j = lane + 64 * i;
+            sv[i] = j < n ? rt<T>(s_lds[h][j]) * kLog2e : -INFINITY;
+            m = fmaxf(m, sv[i]);
+        }
         m = wave_max(m);
         float l = 0.f;
-        for (int j = lane; j < n; j += 64) {
-            const float p = fast_exp2(s_lds[j][h] - m);
-            s_lds[j][h] = p;
+#pragma unroll
+        for (int i = 0; i < kChunk / 64; ++i) {
+            const int j = lane + 64 * i;
+            float p = j < n ? fast_exp2(sv[i] - m) : 0.f;
+            if constexpr (kBf16) {
+                const bf16_t pb = f32_to_bf16(p);
+                p = bf16_to_f32(pb);
+                reinterpret_cast<bf16_t*>(p_lds)[((j >> 1) * G + h) * 2 + (j & 1)] = pb;
+            } else {
+                pf_lds[j * G + h] = p;
+            }
             l += p;
         }
         l = wave_sum(l);
@@ -128,22 +222,43 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(
     }
     __syncthreads();
 
-    // Phase C: unnormalised P @ V.
+    // ---- C: unnormalised P @ V over the chunk
     float o[G][8];
 #pragma unroll
     for (int h = 0; h < G; ++h)
 #pragma unroll
         for (int d = 0; d < 8; ++d) o[h][d] = 0.f;
-    for (int it = 0; it < kChunk / 16; ++it) {
-        const int j = it * 16 + wave * 4 + grp;
-        if (j < n) {
-            float vf[8];
-            load8(V + (int64_t)j * kHeadDim, vf);
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+        const int m = wave * 32 + 4 * t + grp;
+        if constexpr (kBf16) {
+            // interleave rows 2m and 2m+1 per dim: (v_2m[d], v_2m+1[d])
+            const uint32_t* r0 = reinterpret_cast<const uint32_t*>(&vr[t][0].w);
+            const uint32_t* r1 = reinterpret_cast<const uint32_t*>(&vr[t][1].w);
+            uint32_t vv[8];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                vv[2 * i] = __builtin_amdgcn_perm(r1[i], r0[i], 0x05040100u);      // low halves
+                vv[2 * i + 1] = __builtin_amdgcn_perm(r1[i], r0[i], 0x07060302u);  // high halves
+            }
+            const uint32_t* pp = p_lds + m * G;
 #pragma unroll
             for (int h = 0; h < G; ++h) {
-                const float p = s_lds[j][h];
+                const uint32_t pr = pp[h];
 #pragma unroll
-                for (int d = 0; d < 8; ++d) o[h][d] += p * vf[d];
+                for (int d = 0; d < 8; ++d) o[h][d] = dot2(pr, vv[d], o[h][d]);
+            }
+        } else {
+#pragma unroll
+            for (int r = 0; r < 2; ++r) {
+                const float* vf = reinterpret_cast<const float*>(&vr[t][r]);
+                const float* pp = pf_lds + (2 * m + r) * G;
+#pragma unroll
+                for (int h = 0; h < G; ++h) {
+                    const float p = pp[h];
+#pragma unroll
+                    for (int d = 0; d < 8; ++d) o[h][d] += p * vf[d];
+                }
             }
         }
     }
@@ -151,63 +266,56 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(
 #pragma unroll
     for (int h = 0; h < G; ++h)
 #pragma unroll
-        for (int d = 0; d < 8; ++d) {
-            o[h][d] += __shfl_xor(o[h][d], 16);
-            o[h][d] += __shfl_xor(o[h][d], 32);
-        }
+        for (int d = 0; d < 8; ++d) o[h][d] = rows4_sum(o[h][d]);
     if (grp == 0) {
 #pragma unroll
         for (int h = 0; h < G; ++h)
 #pragma unroll
-            for (int d = 0; d < 8; ++d) red[wave][h][8 * l16 + d] = o[h][d];
+            for (int d = 0; d < 8; d += 4)
+                *reinterpret_cast<float4*>(&red[wave][h][8 * l16 + d]) =
+                    make_float4(o[h][d], o[h][d + 1], o[h][d + 2], o[h][d + 3]);
     }
     __syncthreads();
 
     const int n_chunks = (L + kChunk - 1) / kChunk;
-    if (n_chunks == 1) {  // the whole sequence fits one chunk: normalise and finish here
-        for (int e = tid; e < G * kHeadDim; e += kThreads) {
-            const int h = e / kHeadDim, d = e % kHeadDim;
-            const float v = red[0][h][d] + red[1][h][d] + red[2][h][d] + red[3][h][d];
-            Elem<T>::store(out + ((int64_t)b * Hq + h0 + h) * kHeadDim + d, v / ml[h][1]);
-        }
-        return;
-    }
     for (int e = tid; e < G * kHeadDim; e += kThreads) {
         const int h = e / kHeadDim, d = e % kHeadDim;
         const float v = red[0][h][d] + red[1][h][d] + red[2][h][d] + red[3][h][d];
-        ws_o[(((int64_t)b * Hq + h0 + h) * nsplit + c) * kHeadDim + d] = v;
+        if (n_chunks == 1)  // the whole sequence fits one chunk: normalise and finish here
+            Elem<T>::store(out + ((int64_t)b * Hq + h0 + h) * kHeadDim + d, v / ml[h][1]);
+        else
+            ws_o[(((int64_t)b * Hq + h0 + h) * nsplit + c) * kHeadDim + d] = v;
     }
-    if (tid < G) {
+    if (n_chunks > 1 && tid < G) {
         float* dst = ws_ml + (((int64_t)b * Hq + h0 + tid) * nsplit + c) * 2;
         dst[0] = ml[tid][0];
         dst[1] = ml[tid][1];
     }
-    // The last chunk of this (sequence, head group) to finish merges all
-    // partials (log-sum-exp rule) and re-arms the counter for the next call.
-    __threadfence();
-    __syncthreads();
-    __shared__ int is_last;
-    int* counter = counters + (int64_t)b * gridDim.y + blockIdx.y;
-    if (tid == 0) is_last = atomicAdd(counter, 1) == n_chunks - 1;
-    __syncthreads();
-    if (!is_last) return;
-    __threadfence();
-    for (int e = tid; e < G * kHeadDim; e += kThreads) {
-        const int h = e / kHeadDim, d = e % kHeadDim;
-        const int64_t bh = (int64_t)b * Hq + h0 + h;
-        const float* pm = ws_ml + bh * nsplit * 2;
-        const float* po = ws_o + bh * nsplit * kHeadDim + d;
-        float M = -INFINITY;
-        for (int cc = 0; cc < n_chunks; ++cc) M = fmaxf(M, __builtin_nontemporal_load(pm + 2 * cc));
-        float num = 0.f, den = 0.f;
-        for (int cc = 0; cc < n_chunks; ++cc) {
-            const float w = fast_exp2(__builtin_nontemporal_load(pm + 2 * cc) - M);
-            den += w * __builtin_nontemporal_load(pm + 2 * cc + 1);
-            num += w * __builtin_nontemporal_load(po + (int64_t)cc * kHeadDim);
-        }
-        Elem<T>::store(out + bh * kHeadDim + d, num / den);
+}
+
+// Log-sum-exp merge of the chunk partials; one workgroup of 128 threads (one
+// per dim) per (sequence, q head) whose sequence spans more than one chunk.
+template <typename T>
+__global__ __launch_bounds__(kHeadDim) void decode_merge_kernel(
+    const float* __restrict__ ws_o, const float* __restrict__ ws_ml, const int32_t* __restrict__ kv_len,
+    int max_kv, int Hq, int nsplit, T* __restrict__ out) {
+    const int bh = blockIdx.x;
+    const int b = bh / Hq;
+    const int d = threadIdx.x;
+    const int L = min(kv_len[b], max_kv);
+    const int nc = (L + kChunk - 1) / kChunk;
+    if (nc <= 1) return;  // written by the chunk kernel
+    const float* pm = ws_ml + (int64_t)bh * nsplit * 2;
+    const float* po = ws_o + (int64_t)bh * nsplit * kHeadDim + d;
+    float M = -INFINITY;
+    for (int cc = 0; cc < nc; ++cc) M = fmaxf(M, pm[2 * cc]);
+    float num = 0.f, den = 0.f;
+    for (int cc = 0; cc < nc; ++cc) {
+        const float w = fast_exp2(pm[2 * cc] - M);
+        den += w * pm[2 * cc + 1];
+        num += w * po[(int64_t)cc * kHeadDim];
     }
-    if (tid == 0) *counter = 0;
+    Elem<T>::store(out + (int64_t)bh * kHeadDim + d, num / den);
 }
 
 int pick_group(int n_rep) {
@@ -218,16 +326,14 @@ int pick_group(int n_rep) {
 
 template <typename T>
 int launch_decode(const T* q, const T* kc, const T* vc, int64_t cap, const int32_t* kv_len, int max_kv, int nsplit,
-                  int B, int Hq, int Hkv, float scale, float* ws_o, float* ws_ml, int* counters, T* out,
-                  hipStream_t st) {
+                  int B, int Hq, int Hkv, float scale, float* ws_o, float* ws_ml, T* out, hipStream_t st) {
     const int n_rep = Hq / Hkv;
     const int G = pick_group(n_rep);
     const dim3 grid((unsigned)nsplit, (unsigned)(Hkv * (n_rep / G)), (unsigned)B);
-    const float sl = scale * kLog2e;
 #define CRANE_DECODE_CASE(g)                                                                                 \
     case g:                                                                                                  \
-        hipLaunchKernelGGL((decode_split_kernel<T, g>), grid, dim3(kThreads), 0, st, q, kc, vc, cap, kv_len, \
-                           max_kv, Hq, Hkv, n_rep, sl, nsplit, ws_o, ws_ml, counters, out);                 \
+        hipLaunchKernelGGL((decode_chunk_kernel<T, g>), grid, dim3(kThreads), 0, st, q, kc, vc, cap, kv_len, \
+                           max_kv, Hq, Hkv, n_rep, scale, nsplit, ws_o, ws_ml, out);                        \
         break;
     switch (G) {
         CRANE_DECODE_CASE(1)
@@ -241,26 +347,25 @@ int launch_decode(const T* q, const T* kc, const T* vc, int64_t cap, const int32
         default: return CRANE_HIP_E_GQA;
     }
 #undef CRANE_DECODE_CASE
+    if (hipGetLastError() != hipSuccess) return CRANE_HIP_E_LAUNCH;
+    if (nsplit > 1)
+        hipLaunchKernelGGL(decode_merge_kernel<T>, dim3((unsigned)(B * Hq)), dim3(kHeadDim), 0, st, ws_o, ws_ml,
+                           kv_len, max_kv, Hq, nsplit, out);
     return launch_status(hipGetLastError());
 }
 
 int64_t n_splits(int64_t max_kv) { return (max_kv + kChunk - 1) / kChunk; }
 
 struct WsLayout {
-    size_t o_off, ml_off, cnt_off, total;
+    size_t o_off, ml_off, total;
 };
 
-WsLayout ws_layout(int B, int Hq, int Hkv, int64_t ns) {
+WsLayout ws_layout(int B, int Hq, int64_t ns) {
     auto up = [](size_t x) { return (x + 255) & ~(size_t)255; };
     WsLayout w;
-    const size_t o_bytes = (size_t)B * Hq * ns * kHeadDim * sizeof(float);
-    const size_t ml_bytes = (size_t)B * Hq * ns * 2 * sizeof(float);
-    const size_t cnt_bytes = (size_t)B * Hq * sizeof(int);  // >= B * Hkv * (n_rep / G)
-    (void)Hkv;
     w.o_off = 0;
-    w.ml_off = up(o_bytes);
-    w.cnt_off = w.ml_off + up(ml_bytes);
-    w.total = w.cnt_off + up(cnt_bytes);
+    w.ml_off = up((size_t)B * Hq * ns * kHeadDim * sizeof(float));
+    w.total = w.ml_off + up((size_t)B * Hq * ns * 2 * sizeof(float));
     return w;
 }
 
@@ -272,7 +377,7 @@ using namespace crane;
 extern "C" size_t crane_hip_attn_decode_workspace(int B, int Hq, int Hkv, int D, int64_t max_kv, int dtype) {
     (void)dtype;
     if (B <= 0 || Hq <= 0 || Hkv <= 0 || D != kHeadDim || max_kv <= 0) return 0;
-    return ws_layout(B, Hq, Hkv, n_splits(max_kv)).total;
+    return ws_layout(B, Hq, n_splits(max_kv)).total;
 }
 
 extern "C" int crane_hip_attn_decode(const void* q, const void* k_cache, const void* v_cache, int64_t cache_cap,
@@ -289,20 +394,17 @@ extern "C" int crane_hip_attn_decode(const void* q, const void* k_cache, const v
     if (B == 0) return CRANE_HIP_OK;
     if (!q || !k_cache || !v_cache || !kv_len || !out) return CRANE_HIP_E_INVALID;
     if (!aligned16(q) || !aligned16(k_cache) || !aligned16(v_cache)) return CRANE_HIP_E_ALIGN;
-    const size_t need = crane_hip_attn_decode_workspace(B, Hq, Hkv, D, max_kv, dtype);
-    if (!workspace || ws_bytes < need || !aligned16(workspace)) return CRANE_HIP_E_WORKSPACE;
     const int64_t ns = n_splits(max_kv);
-    if (max_kv > 0x7fffffffLL || ns > 0x7fffffffLL || (int64_t)B * Hq > 0x7fffffffLL || B > 65535)
+    if (max_kv > 0x7fffffffLL || ns > 0x7fffffffLL || B > 65535 || (int64_t)B * Hq > 0x7fffffffLL)
         return CRANE_HIP_E_INVALID;
-    const WsLayout w = ws_layout(B, Hq, Hkv, ns);
+    const WsLayout w = ws_layout(B, Hq, ns);
+    if (!workspace || ws_bytes < w.total || !aligned16(workspace)) return CRANE_HIP_E_WORKSPACE;
     float* ws_o = (float*)((char*)workspace + w.o_off);
     float* ws_ml = (float*)((char*)workspace + w.ml_off);
-    int* counters = (int*)((char*)workspace + w.cnt_off);
     hipStream_t st = (hipStream_t)stream;
     if (dtype == CRANE_HIP_F32)
         return launch_decode<float>((const float*)q, (const float*)k_cache, (const float*)v_cache, cache_cap, kv_len,
-                                    (int)max_kv, (int)ns, B, Hq, Hkv, scale, ws_o, ws_ml, counters, (float*)out, st);
+                                    (int)max_kv, (int)ns, B, Hq, Hkv, scale, ws_o, ws_ml, (float*)out, st);
     return launch_decode<bf16_t>((const bf16_t*)q, (const bf16_t*)k_cache, (const bf16_t*)v_cache, cache_cap,
-                                 kv_len, (int)max_kv, (int)ns, B, Hq, Hkv, scale, ws_o, ws_ml, counters,
-                                 (bf16_t*)out, st);
+                                 kv_len, (int)max_kv, (int)ns, B, Hq, Hkv, scale, ws_o, ws_ml, (bf16_t*)out, st);
 }

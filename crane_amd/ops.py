@@ -146,12 +146,12 @@ _WORKSPACES: dict = {}
 
 
 def decode_workspace(device: torch.device, nbytes: int) -> torch.Tensor:
-    """A zero-filled per-(device, stream) workspace, grown on demand.  The decode
-    kernel leaves it zero-filled after each call, so it is reused as is."""
+    """A per-(device, stream) scratch buffer for the split-KV partials, grown on
+    demand; calls on one stream are ordered, so they can share it."""
     key = (device, torch.cuda.current_stream(device).cuda_stream)
     ws = _WORKSPACES.get(key)
     if ws is None or ws.numel() < nbytes:
-        ws = torch.zeros(max(nbytes, 256), dtype=torch.uint8, device=device)
+        ws = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=device)
         _WORKSPACES[key] = ws
     return ws
 

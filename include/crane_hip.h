@@ -110,9 +110,8 @@ size_t crane_hip_attn_decode_workspace(int B, int Hq, int Hkv, int D, int64_t ma
  * scale    softmax scale (1/sqrt(D) in every supported model)
  * out      [B, 1, Hq*D]
  * workspace device scratch of at least crane_hip_attn_decode_workspace(...) bytes,
- *          16-byte aligned, zero-filled before its first use.  Every call leaves
- *          it zero-filled again, so one workspace serves any number of
- *          stream-ordered calls; calls that overlap in time must not share one.
+ *          16-byte aligned, any contents (partial results of the split-KV pass);
+ *          calls that overlap in time must not share a workspace.
  * Replaces: qwen3/modeling.rs:432-467 and :1118-1200 (see the file header). */
 int crane_hip_attn_decode(const void* q, const void* k_cache, const void* v_cache,
                           int64_t cache_cap, const int32_t* kv_len, int64_t max_kv, int B,

@@ -72,3 +72,22 @@ def prefill_case(seed, B, S, Hq, Hkv, start, cap=None, dtype="bf16", poison=True
 def c3_lengths() -> np.ndarray:
     """Config 3: 32 per-sequence lengths uniform in [512, 4096] (seeded)."""
     return rng(SEED0 + 3).integers(512, 4096, size=32, endpoint=True).astype(np.int32)
+
+
+def prefill_truth(q, k, v, start, b, r0, r1, causal=True):
+    """float64 softmax(q K^T / sqrt(D) + mask) V for rows [r0, r1) of sequence b,
+    all heads: [r1 - r0, Hq, D]."""
+    _, Hq, S, _ = q.shape
+    Hkv = k.shape[1]
+    L = int(start[b]) + S
+    out = np.zeros((r1 - r0, Hq, D))
+    for h in range(Hq):
+        K = k[b, h // (Hq // Hkv), :L].astype(np.float64)
+        V = v[b, h // (Hq // Hkv), :L].astype(np.float64)
+        s = q[b, h, r0:r1].astype(np.float64) @ K.T * scale()
+        if causal:
+            pos = int(start[b]) + np.arange(r0, r1)
+            s[np.arange(L)[None, :] > pos[:, None]] = -np.inf
+        p = np.exp(s - s.max(1, keepdims=True))
+        out[:, h] = (p / p.sum(1, keepdims=True)) @ V
+    return out

@@ -76,9 +76,8 @@ def test_decode_workspace_size():
     ns = (4096 + 255) // 256
     o = 32 * 32 * ns * 128 * 4
     ml = 32 * 32 * ns * 2 * 4
-    cnt = 32 * 32 * 4                      # one completion counter per (sequence, head group), padded
     up = lambda x: (x + 255) // 256 * 256
-    assert L.crane_hip_attn_decode_workspace(32, 32, 8, 128, 4096, 1) == up(o) + up(ml) + up(cnt)
+    assert L.crane_hip_attn_decode_workspace(32, 32, 8, 128, 4096, 1) == up(o) + up(ml)
     assert L.crane_hip_attn_decode_workspace(32, 32, 8, 64, 4096, 1) == 0
     assert L.crane_hip_attn_decode_workspace(0, 32, 8, 128, 4096, 1) == 0
 

@@ -28,3 +28,30 @@ def assert_close(x, ref, dtype: str, what: str = ""):
             f"{what}: bf16 max-abs {max_abs:.3e} (<= {BF16_MAX_ABS}), mean-rel {mean_rel:.3e} "
             f"(<= {BF16_MEAN_REL})")
     return max_abs, mean_rel
+
+
+def bf16_ulp(x):
+    """Spacing of bf16 values at |x| (2^(e-7) for x in [2^e, 2^(e+1)))."""
+    a = np.abs(np.asarray(x, dtype=np.float32))
+    e = np.floor(np.log2(np.maximum(a, np.float32(2.0 ** -126))))
+    return np.exp2(e - 7)
+
+
+def assert_ulp_close(x, ref, dtype: str, what: str = "", min_exact: float = 0.9999):
+    """Element-wise parity for the fused append, which reproduces candle's
+    rounding points: bf16 bit-identical almost everywhere (the f32 sum of
+    squares is summed in another order, which can move a normalised value by
+    one ulp; RoPE then carries that ulp, of a value below 16, into the output),
+    so a differing element may be off by at most one bf16 ulp at 8 (2^-4); f32
+    within the f32 parity bar."""
+    x = np.asarray(x, dtype=np.float32)
+    ref = np.asarray(ref, dtype=np.float32)
+    assert np.all(np.isfinite(x)), f"{what}: non-finite output"
+    exact = float(np.mean(x == ref))
+    if dtype == "f32":
+        assert float(np.abs(x - ref).max()) <= F32_MAX_ABS, what
+    else:
+        d = np.abs(x.astype(np.float64) - ref)
+        assert np.all(d <= bf16_ulp(np.maximum(np.abs(ref), 8.0))), f"{what}: differs by more than 2^-4"
+        assert exact >= min_exact, f"{what}: only {exact:.5f} of elements bit-identical"
+    return exact
