@@ -309,6 +309,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--only", choices=["decode", "prefill", "append", "all"], default="all")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="also run a plain 1 GiB device-to-device copy (for scaling FETCH_SIZE/WRITE_SIZE counters)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: the attention path runs on a single MI355X and this build "
@@ -327,6 +329,16 @@ def main():
     stream = torch.cuda.current_stream(dev)
     log(f"device: {torch.cuda.get_device_name(dev)}; lib: {_lib.version()}")
 
+    if args.copy_calibration:
+        import torch
+        src = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        log("[calibration] 3 copies of 1 GiB (1073741824 B read + written each)")
+        del src, dst
+        torch.cuda.empty_cache()
     dec = pre = c5 = c2 = app = None
     if args.only in ("decode", "all"):
         dec = bench_decode(args, dev, stream, lib)

@@ -36,8 +36,13 @@
 namespace crane {
 namespace {
 
-constexpr int kChunk = 256;     // keys per workgroup
-constexpr int kThreads = 256;   // 4 waves
+#ifndef CRANE_DECODE_KROWS
+#define CRANE_DECODE_KROWS 4
+#endif
+constexpr int kChunk = 256;      // keys per workgroup
+constexpr int kThreads = 256;    // 4 waves
+constexpr int kMaxSplits = 4096; // chunks per sequence the merge handles
+constexpr int kKRows = CRANE_DECODE_KROWS;  // K rows in flight per lane in phase A (of 8)
 constexpr int kMaxGroup = 8;    // q heads handled per workgroup
 
 template <int CTRL>
@@ -75,21 +80,23 @@ __device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
     return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_v, a), __builtin_bit_cast(bf16x2_v, b), c, false);
 }
 
-// Storage per lane of one K/V row slice (8 dims).
-template <typename T> struct Row8;
-template <> struct Row8<bf16_t> { uint4 w; };
-template <> struct Row8<float> { float4 a, b; };
+// Buffer resource over `bytes` bytes from `base`: loads outside it return 0,
+// so rows past the end of a chunk need no branch (gfx9 raw buffer, dword3 = 0x00020000).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, int bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, bytes, 0x00020000);
+}
+typedef unsigned int u32x4_v __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ uint4 buf_load16(__amdgpu_buffer_rsrc_t r, int off) {
+    const u32x4_v v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
 
-template <typename T>
-__device__ __forceinline__ Row8<T> load_row8(const T* p, bool valid) {
-    Row8<T> r;
-    if constexpr (std::is_same<T, bf16_t>::value) {
-        r.w = valid ? *reinterpret_cast<const uint4*>(p) : make_uint4(0, 0, 0, 0);
-    } else {
-        r.a = valid ? *reinterpret_cast<const float4*>(p) : make_float4(0, 0, 0, 0);
-        r.b = valid ? *reinterpret_cast<const float4*>(p + 4) : make_float4(0, 0, 0, 0);
-    }
-    return r;
+// Sum over the 8 lanes of a DPP half-row; every lane gets the total.
+__device__ __forceinline__ float row8_sum(float x) {
+    x += dpp<0xB1>(x);   // quad_perm [1,0,3,2]
+    x += dpp<0x4E>(x);   // quad_perm [2,3,0,1]
+    x += dpp<0x141>(x);  // row_half_mirror
+    return x;
 }
 
 // grid: (nsplit, Hkv * (n_rep / G), B).  ws_o: [B, Hq, nsplit, D] f32;
@@ -100,6 +107,8 @@ __global__ __launch_bounds__(kThreads) void decode_chunk_kernel(
     const int32_t* __restrict__ kv_len, int max_kv, int Hq, int Hkv, int n_rep, float scale, int nsplit,
     float* __restrict__ ws_o, float* __restrict__ ws_ml, T* __restrict__ out) {
     constexpr bool kBf16 = std::is_same<T, bf16_t>::value;
+    constexpr int kVecA = 16 * (int)sizeof(T) / 16;  // 16-byte loads per lane per K row (16 dims)
+    constexpr int kVecC = 8 * (int)sizeof(T) / 16;   // 16-byte loads per lane per V row (8 dims)
     const int c = blockIdx.x;
     const int sub_per_kv = n_rep / G;
     const int kvh = blockIdx.y / sub_per_kv;
@@ -115,7 +124,9 @@ __global__ __launch_bounds__(kThreads) void decode_chunk_kernel(
         return;
     }
     const int n = min(kChunk, L - j0);
-    const int lane = tid & 63, wave = tid >> 6, grp = lane >> 4, l16 = lane & 15;
+    const int lane = tid & 63, wave = tid >> 6;
+    const int a8 = lane & 7, r8 = lane >> 3;     // phase A: 8 lanes per key, 16 dims per lane
+    const int grp = lane >> 4, l16 = lane & 15;  // phase C: 16 lanes per key, 8 dims per lane
 
     __shared__ float s_lds[G][kChunk];
     __shared__ uint32_t p_lds[kBf16 ? kChunk / 2 * G : 1];   // bf16 pairs (key 2m, 2m+1) per head
@@ -123,69 +134,75 @@ __global__ __launch_bounds__(kThreads) void decode_chunk_kernel(
     __shared__ __attribute__((aligned(16))) float red[4][G][kHeadDim];
     __shared__ float ml[G][2];
 
-    // q_g = q * scale in T, for this lane's 8 dims of every head.
+    // q_g = q * scale in T, for this lane's 16 dims of every head.
     const float scale_t = rt<T>(scale);
-    uint32_t qp[G][4];
-    float qf[kBf16 ? 1 : G][8];
+    uint32_t qp[kBf16 ? G : 1][8];
+    float qf[kBf16 ? 1 : G][16];
 #pragma unroll
     for (int h = 0; h < G; ++h) {
-        float x[8];
-        load8(q + ((int64_t)b * Hq + h0 + h) * kHeadDim + 8 * l16, x);
+        float x[16];
+        const T* qh = q + ((int64_t)b * Hq + h0 + h) * kHeadDim + 16 * a8;
+        load8(qh, *reinterpret_cast<float(*)[8]>(&x[0]));
+        load8(qh + 8, *reinterpret_cast<float(*)[8]>(&x[8]));
         if constexpr (kBf16) {
 #pragma unroll
-            for (int i = 0; i < 4; ++i) qp[h][i] = pack_bf16x2(x[2 * i] * scale_t, x[2 * i + 1] * scale_t);
+            for (int i = 0; i < 8; ++i) qp[h][i] = pack_bf16x2(x[2 * i] * scale_t, x[2 * i + 1] * scale_t);
         } else {
 #pragma unroll
-            for (int i = 0; i < 8; ++i) qf[h][i] = x[i] * scale_t;
+            for (int i = 0; i < 16; ++i) qf[h][i] = x[i] * scale_t;
         }
     }
-    const int64_t base = (((int64_t)b * Hkv + kvh) * cap + j0) * kHeadDim + 8 * l16;
-    const T* K = kc + base;
-    const T* V = vc + base;
+    // Rows [j0, j0 + n) of this (sequence, kv head); loads past them return 0.
+    const int64_t row0 = ((int64_t)b * Hkv + kvh) * cap + j0;
+    const __amdgpu_buffer_rsrc_t rk = make_rsrc(kc + row0 * kHeadDim, n * kHeadDim * (int)sizeof(T));
+    const __amdgpu_buffer_rsrc_t rv = make_rsrc(vc + row0 * kHeadDim, n * kHeadDim * (int)sizeof(T));
+    constexpr int kRowBytes = kHeadDim * (int)sizeof(T);
 
-    // ---- A: raw scores q_g . k for the chunk; wave w owns keys [64w, 64w+64)
+    // ---- A: raw scores q_g . k; wave w owns keys [64w, 64w+64), 8 keys per load instruction
 #pragma unroll
-    for (int half = 0; half < 2; ++half) {
-        Row8<T> kr[8];
+    for (int half = 0; half < 8 / kKRows; ++half) {
+        uint4 kr[kKRows][kVecA];
 #pragma unroll
-        for (int t = 0; t < 8; ++t) {
-            const int j = wave * 64 + (half * 8 + t) * 4 + grp;
-            kr[t] = load_row8(K + (int64_t)j * kHeadDim, j < n);
+        for (int t = 0; t < kKRows; ++t) {
+            const int j = wave * 64 + (half * kKRows + t) * 8 + r8;
+#pragma unroll
+            for (int v = 0; v < kVecA; ++v) kr[t][v] = buf_load16(rk, j * kRowBytes + 16 * (kVecA * a8 + v));
         }
 #pragma unroll
-        for (int t = 0; t < 8; ++t) {
-            const int j = wave * 64 + (half * 8 + t) * 4 + grp;
+        for (int t = 0; t < kKRows; ++t) {
+            const int j = wave * 64 + (half * kKRows + t) * 8 + r8;
             float acc[G];
 #pragma unroll
             for (int h = 0; h < G; ++h) {
+                float a = 0.f;
                 if constexpr (kBf16) {
-                    float a = dot2(qp[h][0], kr[t].w.x, 0.f);
-                    a = dot2(qp[h][1], kr[t].w.y, a);
-                    a = dot2(qp[h][2], kr[t].w.z, a);
-                    acc[h] = dot2(qp[h][3], kr[t].w.w, a);
-                } else {
-                    const float* kf = reinterpret_cast<const float*>(&kr[t]);
-                    float a = 0.f;
+                    const uint32_t* kw = reinterpret_cast<const uint32_t*>(&kr[t][0]);
 #pragma unroll
-                    for (int i = 0; i < 8; ++i) a += qf[h][i] * kf[i];
-                    acc[h] = a;
+                    for (int i = 0; i < 8; ++i) a = dot2(qp[h][i], kw[i], a);
+                } else {
+                    const float* kf = reinterpret_cast<const float*>(&kr[t][0]);
+#pragma unroll
+                    for (int i = 0; i < 16; ++i) a += qf[h][i] * kf[i];
                 }
-                acc[h] = row16_sum(acc[h]);
+                acc[h] = row8_sum(a);
             }
             float mine = acc[0];
 #pragma unroll
-            for (int h = 1; h < G; ++h) mine = l16 == h ? acc[h] : mine;
-            if (l16 < G && j < n) s_lds[l16][j] = mine;
+            for (int h = 1; h < G; ++h) mine = a8 == h ? acc[h] : mine;
+            if (a8 < G && j < n) s_lds[a8][j] = mine;
         }
     }
 
     // Prefetch this lane's V rows for C while B runs: pairs m = 32w + 4t + grp.
-    Row8<T> vr[8][2];
+    uint4 vr[8][2][kVecC];
 #pragma unroll
     for (int t = 0; t < 8; ++t) {
         const int m = wave * 32 + 4 * t + grp;
 #pragma unroll
-        for (int r = 0; r < 2; ++r) vr[t][r] = load_row8(V + (int64_t)(2 * m + r) * kHeadDim, 2 * m + r < n);
+        for (int r = 0; r < 2; ++r)
+#pragma unroll
+            for (int v = 0; v < kVecC; ++v)
+                vr[t][r][v] = buf_load16(rv, (2 * m + r) * kRowBytes + 16 * (kVecC * l16 + v));
     }
     __syncthreads();
 
@@ -222,7 +239,7 @@ __global__ __launch_bounds__(kThreads) void decode_chunk_kernel(
     }
     __syncthreads();
 
-    // ---- C: unnormalised P @ V over the chunk
+    // ---- C: unnormalised P @ V over the chunk (rows past n were read as 0, p = 0)
     float o[G][8];
 #pragma unroll
     for (int h = 0; h < G; ++h)
@@ -233,8 +250,8 @@ __global__ __launch_bounds__(kThreads) void decode_chunk_kernel(
         const int m = wave * 32 + 4 * t + grp;
         if constexpr (kBf16) {
             // interleave rows 2m and 2m+1 per dim: (v_2m[d], v_2m+1[d])
-            const uint32_t* r0 = reinterpret_cast<const uint32_t*>(&vr[t][0].w);
-            const uint32_t* r1 = reinterpret_cast<const uint32_t*>(&vr[t][1].w);
+            const uint32_t* r0 = reinterpret_cast<const uint32_t*>(&vr[t][0][0]);
+            const uint32_t* r1 = reinterpret_cast<const uint32_t*>(&vr[t][1][0]);
             uint32_t vv[8];
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
@@ -251,7 +268,7 @@ __global__ __launch_bounds__(kThreads) void decode_chunk_kernel(
         } else {
 #pragma unroll
             for (int r = 0; r < 2; ++r) {
-                const float* vf = reinterpret_cast<const float*>(&vr[t][r]);
+                const float* vf = reinterpret_cast<const float*>(&vr[t][r][0]);
                 const float* pp = pf_lds + (2 * m + r) * G;
 #pragma unroll
                 for (int h = 0; h < G; ++h) {
@@ -293,28 +310,54 @@ __global__ __launch_bounds__(kThreads) void decode_chunk_kernel(
     }
 }
 
-// Log-sum-exp merge of the chunk partials; one workgroup of 128 threads (one
+// Log-sum-exp merge of the chunk partials: one workgroup of 128 threads (one
 // per dim) per (sequence, q head) whose sequence spans more than one chunk.
+// The chunk weights are computed once in LDS; the partial rows are then read
+// with independent, coalesced loads.
 template <typename T>
 __global__ __launch_bounds__(kHeadDim) void decode_merge_kernel(
     const float* __restrict__ ws_o, const float* __restrict__ ws_ml, const int32_t* __restrict__ kv_len,
     int max_kv, int Hq, int nsplit, T* __restrict__ out) {
+    constexpr int chunk = kChunk;
+    __shared__ float w_lds[kMaxSplits];
+    __shared__ float red[2];
     const int bh = blockIdx.x;
     const int b = bh / Hq;
     const int d = threadIdx.x;
     const int L = min(kv_len[b], max_kv);
-    const int nc = (L + kChunk - 1) / kChunk;
-    if (nc <= 1) return;  // written by the chunk kernel
+    const int nc = (L + chunk - 1) / chunk;
+    if (nc <= 1) return;  // written by the split kernel
     const float* pm = ws_ml + (int64_t)bh * nsplit * 2;
     const float* po = ws_o + (int64_t)bh * nsplit * kHeadDim + d;
-    float M = -INFINITY;
-    for (int cc = 0; cc < nc; ++cc) M = fmaxf(M, pm[2 * cc]);
-    float num = 0.f, den = 0.f;
-    for (int cc = 0; cc < nc; ++cc) {
+    float mx = -INFINITY;
+    for (int cc = d; cc < nc; cc += kHeadDim) mx = fmaxf(mx, pm[2 * cc]);
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) mx = fmaxf(mx, __shfl_xor(mx, m));
+    if ((d & 63) == 0) red[d >> 6] = mx;
+    __syncthreads();
+    const float M = fmaxf(red[0], red[1]);
+    float den = 0.f;
+    for (int cc = d; cc < nc; cc += kHeadDim) {
         const float w = fast_exp2(pm[2 * cc] - M);
+        w_lds[cc] = w;
         den += w * pm[2 * cc + 1];
-        num += w * po[(int64_t)cc * kHeadDim];
     }
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) den += __shfl_xor(den, m);
+    __syncthreads();
+    if ((d & 63) == 0) red[d >> 6] = den;
+    __syncthreads();
+    den = red[0] + red[1];
+    float num = 0.f;
+    int cc = 0;
+    for (; cc + 8 <= nc; cc += 8) {
+        float x[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) x[i] = po[(int64_t)(cc + i) * kHeadDim];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) num += w_lds[cc + i] * x[i];
+    }
+    for (; cc < nc; ++cc) num += w_lds[cc] * po[(int64_t)cc * kHeadDim];
     Elem<T>::store(out + (int64_t)bh * kHeadDim + d, num / den);
 }
 

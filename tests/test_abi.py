@@ -71,13 +71,29 @@ def test_decode_argument_checks(kw, code):
     assert _decode(**kw) == code
 
 
-def test_decode_workspace_size():
+def _chunk(B, Hq, Hkv, max_kv):
+    """Keys per decode workgroup: the largest power-of-two multiple (<= 16) of
+    256 leaving >= 2048 workgroups for the longest sequence."""
+    n_rep = Hq // Hkv
+    g = max(x for x in range(1, 9) if n_rep % x == 0)
+    groups = B * Hkv * (n_rep // g)
+    chunk = 256
+    while chunk < 16 * 256 and groups * ((max_kv + 2 * chunk - 1) // (2 * chunk)) >= 2048:
+        chunk *= 2
+    return chunk
+
+
+@pytest.mark.parametrize("B,Hq,Hkv,max_kv,chunk", [
+    (32, 32, 8, 4097, 512),     # config 3
+    (8, 64, 8, 32769, 1024),    # config 5
+    (1, 16, 8, 1025, 256),      # config 1
+])
+def test_decode_workspace_size(B, Hq, Hkv, max_kv, chunk):
     L = _lib.lib()
-    ns = (4096 + 255) // 256
-    o = 32 * 32 * ns * 128 * 4
-    ml = 32 * 32 * ns * 2 * 4
+    assert _chunk(B, Hq, Hkv, max_kv) == chunk
+    ns = (max_kv + chunk - 1) // chunk
     up = lambda x: (x + 255) // 256 * 256
-    assert L.crane_hip_attn_decode_workspace(32, 32, 8, 128, 4096, 1) == up(o) + up(ml)
+    assert L.crane_hip_attn_decode_workspace(B, Hq, Hkv, 128, max_kv, 1) == up(B * Hq * ns * 128 * 4) + up(B * Hq * ns * 8)
     assert L.crane_hip_attn_decode_workspace(32, 32, 8, 64, 4096, 1) == 0
     assert L.crane_hip_attn_decode_workspace(0, 32, 8, 128, 4096, 1) == 0
 
