@@ -8,20 +8,23 @@
 // softmax as padding with masked columns (exp(-1e9 - m) == 0 in f32).
 //
 // Kernel 1 (decode_chunk_kernel): one workgroup (4 waves) per (chunk of 256
-// keys, kv head, sequence).  The G query heads sharing the kv head are done
-// together, so each K/V row is read from HBM once for the whole GQA group, and
-// no MFMA is used: the path is HBM-bound.
-//   A. scores: 16 lanes read one K row with one 16-byte load each (a wave load
-//      instruction covers 4 consecutive rows, 1 KiB); each lane does the dot
-//      product of its 8 dims with v_dot2_f32_bf16 for all G heads, and a
-//      4-step DPP butterfly inside the 16-lane row completes it.
+// keys, kv head group, sequence).  The G query heads sharing the kv head are
+// done together, so each K/V row is read from HBM once for the whole GQA
+// group, and no MFMA is used: the path is HBM-bound.  Rows are read with
+// bounds-checked buffer loads (rows past the sequence end read as zero, so no
+// branch guards a load).
+//   A. scores: 8 lanes read one K row (two 16-byte loads each, 16 dims per
+//      lane; a wave covers 8 rows per load pair), each lane does the dot
+//      product of its 16 dims with v_dot2_f32_bf16 for all G heads, and a
+//      3-step DPP butterfly inside the 8 lanes completes it.
 //   B. the chunk's softmax statistics per head (max m and sum l of the
-//      bf16-rounded exp2(s - m), log2 domain), computed once per (head, key);
-//      probabilities go to LDS as packed bf16 pairs of consecutive keys.
-//   C. P @ V: 16 lanes read a V row; two consecutive rows are interleaved
-//      with v_perm so v_dot2_f32_bf16 takes (p_j, p_j+1) x (v_j, v_j+1) per
-//      dim.  The 4 row groups of a wave are summed with lane permutes and
-//      the 4 waves through LDS.
+//      bf16-rounded exp2(s - m), log2 domain), computed once per (head, key)
+//      with DPP wave reductions; probabilities go to LDS as packed bf16 pairs
+//      of consecutive keys.
+//   C. P @ V: 16 lanes read a V row (8 dims each); two consecutive rows are
+//      interleaved with v_perm so v_dot2_f32_bf16 takes (p_j, p_j+1) x
+//      (v_j, v_j+1) per dim.  The 4 row groups of a wave are summed with lane
+//      permutes and the 4 waves through LDS.
 // A sequence that fits one chunk is normalised and written directly; longer
 // ones leave their unnormalised f32 partial and (m, l) in the workspace.
 // Kernel 2 (decode_merge_kernel): the log-sum-exp merge of those partials.
@@ -39,7 +42,19 @@ namespace {
 #ifndef CRANE_DECODE_KROWS
 #define CRANE_DECODE_KROWS 4
 #endif
-constexpr int kChunk = 256;      // keys per workgroup
+#ifndef CRANE_DECODE_CHUNK
+#define CRANE_DECODE_CHUNK 256
+#endif
+constexpr int kChunk = CRANE_DECODE_CHUNK;  // keys per workgroup (128 or 256)
+#ifndef CRANE_DECODE_EARLYV
+#define CRANE_DECODE_EARLYV 0
+#endif
+#ifndef CRANE_DECODE_CL
+#define CRANE_DECODE_CL 2
+#endif
+constexpr int kCL = CRANE_DECODE_CL;        // adjacent chunks dispatched together
+constexpr int kStepsA = kChunk / 32;        // 8-key row steps per wave in phase A
+constexpr int kPairsC = kChunk / 32;        // key pairs per 16-lane group in phase C
 constexpr int kThreads = 256;    // 4 waves
 constexpr int kMaxSplits = 4096; // chunks per sequence the merge handles
 constexpr int kKRows = CRANE_DECODE_KROWS;  // K rows in flight per lane in phase A (of 8)
@@ -65,15 +80,27 @@ __device__ __forceinline__ float rows4_sum(float x) {
     return x + __shfl_xor(x, 32);
 }
 
+// Whole-wave max / sum with DPP: reduce each 16-lane row, fold the rows with
+// row_bcast:15 / row_bcast:31 into lane 63, and broadcast it with readlane.
+template <int CTRL, int ROWS>
+__device__ __forceinline__ float dpp_rows(float x, float identity) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, identity),
+                                                                 __builtin_bit_cast(int, x), CTRL, ROWS, 0xf, false));
+}
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m));
-    return v;
+    v = fmaxf(v, dpp<0xB1>(v));
+    v = fmaxf(v, dpp<0x4E>(v));
+    v = fmaxf(v, dpp<0x124>(v));
+    v = fmaxf(v, dpp<0x128>(v));
+    v = fmaxf(v, dpp_rows<0x142, 0xa>(v, -INFINITY));  // row_bcast:15 into rows 1, 3
+    v = fmaxf(v, dpp_rows<0x143, 0xc>(v, -INFINITY));  // row_bcast:31 into rows 2, 3
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
 }
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m);
-    return v;
+    v = row16_sum(v);
+    v += dpp_rows<0x142, 0xa>(v, 0.f);
+    v += dpp_rows<0x143, 0xc>(v, 0.f);
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
 }
 
 __device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
@@ -99,22 +126,30 @@ __device__ __forceinline__ float row8_sum(float x) {
     return x;
 }
 
-// grid: (nsplit, Hkv * (n_rep / G), B).  ws_o: [B, Hq, nsplit, D] f32;
-// ws_ml: [B, Hq, nsplit, 2] f32 (max, sum) in the log2 domain.
 template <typename T, int G>
-__global__ __launch_bounds__(kThreads) void decode_chunk_kernel(
-    const T* __restrict__ q, const T* __restrict__ kc, const T* __restrict__ vc, int64_t cap,
-    const int32_t* __restrict__ kv_len, int max_kv, int Hq, int Hkv, int n_rep, float scale, int nsplit,
+struct DecodeShared {
+    static constexpr bool kBf16 = std::is_same<T, bf16_t>::value;
+    float s[G][kChunk];                                  // raw scores
+    uint32_t p[kBf16 ? kChunk / 2 * G : 1];              // bf16 probability pairs (key 2m, 2m+1) per head
+    float pf[kBf16 ? 1 : kChunk * G];                    // f32 probabilities
+    __attribute__((aligned(16))) float red[4][G][kHeadDim];  // per-wave partial rows
+    float ml[G][2];                                      // chunk (max, sum) per head
+};
+
+// One work item: chunk c (keys [c kChunk, (c+1) kChunk)) of sequence b for the
+// G q heads of head group gi.  Writes the normalised rows when the sequence
+// fits one chunk, otherwise the unnormalised partial and its (max, sum).
+template <typename T, int G>
+__device__ __forceinline__ void decode_item(
+    DecodeShared<T, G>& sm, const T* __restrict__ q, const T* __restrict__ kc, const T* __restrict__ vc,
+    int64_t cap, int L, int b, int gi, int c, int Hq, int Hkv, int n_rep, float scale, int nsplit,
     float* __restrict__ ws_o, float* __restrict__ ws_ml, T* __restrict__ out) {
     constexpr bool kBf16 = std::is_same<T, bf16_t>::value;
     constexpr int kVecA = 16 * (int)sizeof(T) / 16;  // 16-byte loads per lane per K row (16 dims)
     constexpr int kVecC = 8 * (int)sizeof(T) / 16;   // 16-byte loads per lane per V row (8 dims)
-    const int c = blockIdx.x;
     const int sub_per_kv = n_rep / G;
-    const int kvh = blockIdx.y / sub_per_kv;
-    const int h0 = kvh * n_rep + (blockIdx.y % sub_per_kv) * G;  // first q head of this group
-    const int b = blockIdx.z;
-    const int L = min(kv_len[b], max_kv);  // never read past the rows the host vouched for
+    const int kvh = gi / sub_per_kv;
+    const int h0 = kvh * n_rep + (gi % sub_per_kv) * G;  // first q head of this group
     const int j0 = c * kChunk;
     const int tid = threadIdx.x;
     if (j0 >= L) {  // uniform over the workgroup
@@ -127,12 +162,11 @@ __global__ __launch_bounds__(kThreads) void decode_chunk_kernel(
     const int lane = tid & 63, wave = tid >> 6;
     const int a8 = lane & 7, r8 = lane >> 3;     // phase A: 8 lanes per key, 16 dims per lane
     const int grp = lane >> 4, l16 = lane & 15;  // phase C: 16 lanes per key, 8 dims per lane
-
-    __shared__ float s_lds[G][kChunk];
-    __shared__ uint32_t p_lds[kBf16 ? kChunk / 2 * G : 1];   // bf16 pairs (key 2m, 2m+1) per head
-    __shared__ float pf_lds[kBf16 ? 1 : kChunk * G];          // f32 probabilities
-    __shared__ __attribute__((aligned(16))) float red[4][G][kHeadDim];
-    __shared__ float ml[G][2];
+    auto& s_lds = sm.s;
+    uint32_t* p_lds = sm.p;
+    float* pf_lds = sm.pf;
+    auto& red = sm.red;
+    auto& ml = sm.ml;
 
     // q_g = q * scale in T, for this lane's 16 dims of every head.
     const float scale_t = rt<T>(scale);
@@ -158,19 +192,32 @@ __global__ __launch_bounds__(kThreads) void decode_chunk_kernel(
     const __amdgpu_buffer_rsrc_t rv = make_rsrc(vc + row0 * kHeadDim, n * kHeadDim * (int)sizeof(T));
     constexpr int kRowBytes = kHeadDim * (int)sizeof(T);
 
-    // ---- A: raw scores q_g . k; wave w owns keys [64w, 64w+64), 8 keys per load instruction
+#if CRANE_DECODE_EARLYV
+    // V rows for C, issued before phase A: pairs m = w kChunk/8 + 4t + grp.
+    uint4 vr[kPairsC][2][kVecC];
 #pragma unroll
-    for (int half = 0; half < 8 / kKRows; ++half) {
+    for (int t = 0; t < kPairsC; ++t) {
+        const int m = wave * (kChunk / 8) + 4 * t + grp;
+#pragma unroll
+        for (int r = 0; r < 2; ++r)
+#pragma unroll
+            for (int v = 0; v < kVecC; ++v)
+                vr[t][r][v] = buf_load16(rv, (2 * m + r) * kRowBytes + 16 * (kVecC * l16 + v));
+    }
+#endif
+    // ---- A: raw scores q_g . k; wave w owns keys [w kChunk/4, (w+1) kChunk/4), 8 per load instruction
+#pragma unroll
+    for (int half = 0; half < kStepsA / kKRows; ++half) {
         uint4 kr[kKRows][kVecA];
 #pragma unroll
         for (int t = 0; t < kKRows; ++t) {
-            const int j = wave * 64 + (half * kKRows + t) * 8 + r8;
+            const int j = wave * (kChunk / 4) + (half * kKRows + t) * 8 + r8;
 #pragma unroll
             for (int v = 0; v < kVecA; ++v) kr[t][v] = buf_load16(rk, j * kRowBytes + 16 * (kVecA * a8 + v));
         }
 #pragma unroll
         for (int t = 0; t < kKRows; ++t) {
-            const int j = wave * 64 + (half * kKRows + t) * 8 + r8;
+            const int j = wave * (kChunk / 4) + (half * kKRows + t) * 8 + r8;
             float acc[G];
 #pragma unroll
             for (int h = 0; h < G; ++h) {
@@ -193,17 +240,19 @@ __global__ __launch_bounds__(kThreads) void decode_chunk_kernel(
         }
     }
 
-    // Prefetch this lane's V rows for C while B runs: pairs m = 32w + 4t + grp.
-    uint4 vr[8][2][kVecC];
+#if !CRANE_DECODE_EARLYV
+    // Prefetch this lane's V rows for C while B runs: pairs m = w kChunk/8 + 4t + grp.
+    uint4 vr[kPairsC][2][kVecC];
 #pragma unroll
-    for (int t = 0; t < 8; ++t) {
-        const int m = wave * 32 + 4 * t + grp;
+    for (int t = 0; t < kPairsC; ++t) {
+        const int m = wave * (kChunk / 8) + 4 * t + grp;
 #pragma unroll
         for (int r = 0; r < 2; ++r)
 #pragma unroll
             for (int v = 0; v < kVecC; ++v)
                 vr[t][r][v] = buf_load16(rv, (2 * m + r) * kRowBytes + 16 * (kVecC * l16 + v));
     }
+#endif
     __syncthreads();
 
     // ---- B: per-head chunk max and sum (log2 domain); probabilities to LDS
@@ -246,8 +295,8 @@ __global__ __launch_bounds__(kThreads) void decode_chunk_kernel(
 #pragma unroll
         for (int d = 0; d < 8; ++d) o[h][d] = 0.f;
 #pragma unroll
-    for (int t = 0; t < 8; ++t) {
-        const int m = wave * 32 + 4 * t + grp;
+    for (int t = 0; t < kPairsC; ++t) {
+        const int m = wave * (kChunk / 8) + 4 * t + grp;
         if constexpr (kBf16) {
             // interleave rows 2m and 2m+1 per dim: (v_2m[d], v_2m+1[d])
             const uint32_t* r0 = reinterpret_cast<const uint32_t*>(&vr[t][0][0]);
@@ -310,6 +359,25 @@ __global__ __launch_bounds__(kThreads) void decode_chunk_kernel(
     }
 }
 
+// Dispatch order: blocks of kCL adjacent chunks of one head group are
+// consecutive (adjacent cache rows are read together) and the block index is
+// the slowest grid dimension, so every sequence's first chunks go first and the
+// workgroups past the shorter sequences' ends (which exit at once) come last
+// instead of being interleaved.  grid: (groups * kCL, B, ceil(nsplit / kCL)).
+template <typename T, int G>
+__global__ __launch_bounds__(kThreads) void decode_chunk_kernel(
+    const T* __restrict__ q, const T* __restrict__ kc, const T* __restrict__ vc, int64_t cap,
+    const int32_t* __restrict__ kv_len, int max_kv, int Hq, int Hkv, int n_rep, float scale, int nsplit,
+    float* __restrict__ ws_o, float* __restrict__ ws_ml, T* __restrict__ out) {
+    __shared__ DecodeShared<T, G> sm;
+    const int c = blockIdx.z * kCL + (int)(blockIdx.x % kCL);
+    if (c >= nsplit) return;
+    const int b = blockIdx.y;
+    const int L = min(kv_len[b], max_kv);  // never read past the rows the host vouched for
+    decode_item<T, G>(sm, q, kc, vc, cap, L, b, blockIdx.x / kCL, c, Hq, Hkv, n_rep, scale, nsplit, ws_o, ws_ml,
+                      out);
+}
+
 // Log-sum-exp merge of the chunk partials: one workgroup of 128 threads (one
 // per dim) per (sequence, q head) whose sequence spans more than one chunk.
 // The chunk weights are computed once in LDS; the partial rows are then read
@@ -367,18 +435,28 @@ int pick_group(int n_rep) {
     return 1;
 }
 
+template <typename T, int G>
+int launch_decode_g(const T* q, const T* kc, const T* vc, int64_t cap, const int32_t* kv_len, int max_kv,
+                    int nsplit, int B, int Hq, int Hkv, float scale, float* ws_o, float* ws_ml, T* out,
+                    hipStream_t st) {
+    const int n_rep = Hq / Hkv;
+    const int groups = Hkv * (n_rep / G);
+    const dim3 grid((unsigned)(groups * kCL), (unsigned)B, (unsigned)((nsplit + kCL - 1) / kCL));
+    hipLaunchKernelGGL((decode_chunk_kernel<T, G>), grid, dim3(kThreads), 0, st, q, kc, vc, cap, kv_len, max_kv,
+                       Hq, Hkv, n_rep, scale, nsplit, ws_o, ws_ml, out);
+    return hipGetLastError() == hipSuccess ? CRANE_HIP_OK : CRANE_HIP_E_LAUNCH;
+}
+
 template <typename T>
 int launch_decode(const T* q, const T* kc, const T* vc, int64_t cap, const int32_t* kv_len, int max_kv, int nsplit,
                   int B, int Hq, int Hkv, float scale, float* ws_o, float* ws_ml, T* out, hipStream_t st) {
-    const int n_rep = Hq / Hkv;
-    const int G = pick_group(n_rep);
-    const dim3 grid((unsigned)nsplit, (unsigned)(Hkv * (n_rep / G)), (unsigned)B);
-#define CRANE_DECODE_CASE(g)                                                                                 \
-    case g:                                                                                                  \
-        hipLaunchKernelGGL((decode_chunk_kernel<T, g>), grid, dim3(kThreads), 0, st, q, kc, vc, cap, kv_len, \
-                           max_kv, Hq, Hkv, n_rep, scale, nsplit, ws_o, ws_ml, out);                        \
+    int rc;
+    switch (pick_group(Hq / Hkv)) {
+#define CRANE_DECODE_CASE(g)                                                                                      \
+    case g:                                                                                                       \
+        rc = launch_decode_g<T, g>(q, kc, vc, cap, kv_len, max_kv, nsplit, B, Hq, Hkv, scale, ws_o, ws_ml, out,  \
+                                   st);                                                                           \
         break;
-    switch (G) {
         CRANE_DECODE_CASE(1)
         CRANE_DECODE_CASE(2)
         CRANE_DECODE_CASE(3)
@@ -387,10 +465,10 @@ int launch_decode(const T* q, const T* kc, const T* vc, int64_t cap, const int32
         CRANE_DECODE_CASE(6)
         CRANE_DECODE_CASE(7)
         CRANE_DECODE_CASE(8)
+#undef CRANE_DECODE_CASE
         default: return CRANE_HIP_E_GQA;
     }
-#undef CRANE_DECODE_CASE
-    if (hipGetLastError() != hipSuccess) return CRANE_HIP_E_LAUNCH;
+    if (rc != CRANE_HIP_OK) return rc;
     if (nsplit > 1)
         hipLaunchKernelGGL(decode_merge_kernel<T>, dim3((unsigned)(B * Hq)), dim3(kHeadDim), 0, st, ws_o, ws_ml,
                            kv_len, max_kv, Hq, nsplit, out);
@@ -399,6 +477,7 @@ int launch_decode(const T* q, const T* kc, const T* vc, int64_t cap, const int32
 
 int64_t n_splits(int64_t max_kv) { return (max_kv + kChunk - 1) / kChunk; }
 
+// Workspace: the partial rows, then their (max, sum) pairs.
 struct WsLayout {
     size_t o_off, ml_off, total;
 };
@@ -407,7 +486,7 @@ WsLayout ws_layout(int B, int Hq, int64_t ns) {
     auto up = [](size_t x) { return (x + 255) & ~(size_t)255; };
     WsLayout w;
     w.o_off = 0;
-    w.ml_off = up((size_t)B * Hq * ns * kHeadDim * sizeof(float));
+    w.ml_off = w.o_off + up((size_t)B * Hq * ns * kHeadDim * sizeof(float));
     w.total = w.ml_off + up((size_t)B * Hq * ns * 2 * sizeof(float));
     return w;
 }
@@ -438,7 +517,7 @@ extern "C" int crane_hip_attn_decode(const void* q, const void* k_cache, const v
     if (!q || !k_cache || !v_cache || !kv_len || !out) return CRANE_HIP_E_INVALID;
     if (!aligned16(q) || !aligned16(k_cache) || !aligned16(v_cache)) return CRANE_HIP_E_ALIGN;
     const int64_t ns = n_splits(max_kv);
-    if (max_kv > 0x7fffffffLL || ns > 0x7fffffffLL || B > 65535 || (int64_t)B * Hq > 0x7fffffffLL)
+    if (max_kv > 0x7fffffffLL || ns > kMaxSplits || B > 65535 || (int64_t)B * Hq > 0x7fffffffLL)
         return CRANE_HIP_E_INVALID;
     const WsLayout w = ws_layout(B, Hq, ns);
     if (!workspace || ws_bytes < w.total || !aligned16(workspace)) return CRANE_HIP_E_WORKSPACE;

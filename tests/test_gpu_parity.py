@@ -221,3 +221,31 @@ def test_prefill_last_row_equals_decode(gpu):
     pre = host(ops.attention_prefill(qd, kd, vd, i32(st, gpu), 0))
     dec = host(ops.attention_decode(qd[:, :, -1].contiguous(), kd, vd, i32([333, 333], gpu), 333))
     assert np.max(np.abs(pre[:, -1] - dec[:, 0])) <= 2e-2
+
+
+def test_decode_workspace_reuse_across_shapes(gpu, orc):
+    """One workspace serves successive calls of different shapes."""
+    from crane_amd import ops
+    ws = torch.zeros(ops.decode_workspace_bytes(8, 32, 8, 3000) + 4096, dtype=torch.uint8, device=gpu)
+    for i, (B, Hq, Hkv, lens) in enumerate([(8, 32, 8, [3000, 1, 700, 2999, 256, 257, 1024, 77]),
+                                             (3, 8, 2, [5, 600, 2048]), (8, 32, 8, [100] * 8)]):
+        note(f"workspace reuse call {i}: B={B} lens={lens}")
+        q, k, v, lens = cases.decode_case(400 + i, B, Hq, Hkv, lens, dtype="bf16")
+        out = host(ops.attention_decode(dev_t(q, "bf16", gpu), dev_t(k, "bf16", gpu), dev_t(v, "bf16", gpu),
+                                        i32(lens, gpu), int(lens.max()), workspace=ws)).reshape(B, Hq * D)
+        ref = orc.attn_decode(q, k, v, lens, cases.scale(), "bf16")
+        assert_close(out, ref, "bf16", f"reuse call {i}")
+
+
+def test_decode_large_batch(gpu, orc):
+    """A batch of 1100 ragged sequences, some of them empty."""
+    from crane_amd import ops
+    B, Hq, Hkv = 1100, 4, 2
+    lens = cases.rng(55).integers(0, 600, size=B).astype(np.int32)
+    note(f"decode large batch: B={B} max_len={lens.max()}")
+    q, k, v, lens = cases.decode_case(56, B, Hq, Hkv, lens, dtype="bf16")
+    out = host(ops.attention_decode(dev_t(q, "bf16", gpu), dev_t(k, "bf16", gpu), dev_t(v, "bf16", gpu),
+                                    i32(lens, gpu), int(lens.max()))).reshape(B, Hq * D)
+    ref = orc.attn_decode(q, k, v, lens, cases.scale(), "bf16")
+    assert np.all(out[lens == 0] == 0)
+    assert_close(out, ref, "bf16", "large batch")
