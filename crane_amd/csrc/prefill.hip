@@ -13,9 +13,13 @@
 // so a lane holds 16 keys of ONE query row (lane%32) and the row max/sum need
 // one cross-half exchange only.  The resulting P^T tile is already laid out as
 // the B operand of O^T = V^T P^T: no data movement between the two products.
-// K is staged in LDS row-major ([key][dim], A operand of the first product);
-// V is staged transposed ([dim][key]) so that each A-operand fragment of the
-// second product is two 8-byte LDS reads.  LDS rows are padded to spread banks.
+// K and V tiles are copied HBM -> LDS row-major, as Crane stores them, by
+// bounds-checked buffer_load ... lds (no VGPRs, no VALU, zero rows past the
+// cache end), double-buffered so tile t+1 is in flight while tile t is
+// computed.  K rows are the A operand of the first product; the second
+// product's A operand V^T comes from the same row-major tile through
+// ds_read_b64_tr_b16 transposed reads.  16-byte chunks are XOR-swizzled per
+// row so both read patterns avoid LDS bank conflicts.
 // Workgroup ids are remapped so that heavy (late) query tiles start first and
 // the q heads sharing a kv head run on the same XCD (shared L2).
 //
@@ -27,16 +31,54 @@
 namespace crane {
 namespace {
 
-constexpr int kBM = 128;           // query rows per workgroup
-constexpr int kBN = 64;            // keys per tile
-constexpr int kKStride = 128 + 8;  // bf16 elements per K row in LDS (272 B)
-constexpr int kVStride = kBN + 4;  // bf16 elements per V^T row in LDS (136 B)
+constexpr int kBM = 128;                      // query rows per workgroup
+constexpr int kBN = 64;                       // keys per tile
+constexpr int kTileBytes = kBN * kHeadDim * 2;  // 16 KiB of K (or V) per tile
+constexpr float kLazy = 8.0f;                 // log2-domain slack before the running max moves
 
 __device__ __forceinline__ f32x16_v mfma32(bf16x8_v a, bf16x8_v b, f32x16_v c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
 }
 
 __device__ __forceinline__ bf16x8_v as_bf16x8(uint4 u) { return __builtin_bit_cast(bf16x8_v, u); }
+
+// LDS tiles keep Crane's row-major rows (256 B per key) with the 16-byte chunks
+// of row r XOR-permuted by swz(r): 16 consecutive rows read at one chunk index
+// (K fragments) hit 16 different chunks, and the 4-row x 2-chunk blocks of the
+// transposed V reads hit 8 different chunks.
+__device__ __forceinline__ int swz(int row) { return ((row & 3) << 1) | ((row >> 2) & 1) | (((row >> 3) & 1) << 3); }
+
+typedef __attribute__((__vector_size__(4 * sizeof(short)))) short s16x4_v;
+typedef __attribute__((address_space(3))) s16x4_v lds_s16x4_v;
+
+// ds_read_b64_tr_b16: within each 16-lane group, lane i supplies 4 consecutive
+// bf16 x[i][0..3] and receives x[4k + i/4][i%4] for k = 0..3.  With lane i
+// pointing at row base + i/4, columns c0 + 4(i%4) .. +3 of a row-major tile,
+// lane i receives column c0 + i of rows base .. base + 3: a transposed read.
+__device__ __forceinline__ uint2 read_tr16(const uint8_t* p) {
+    const s16x4_v v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_v*)(p));
+    return __builtin_bit_cast(uint2, v);
+}
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, int bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, bytes, 0x00020000);
+}
+
+// Copy keys [64 t, 64 t + 64) of K and V into one LDS stage with
+// bounds-checked buffer_load ... lds (rows past the cache rows read as zero).
+// Wave w copies the 1 KiB blocks 4w..4w+3 of each tile; lane l of block blk
+// fills row 4 blk + l/16, chunk l%16, with global chunk (l%16) ^ swz(row).
+__device__ __forceinline__ void issue_tile(__amdgpu_buffer_rsrc_t rk, __amdgpu_buffer_rsrc_t rv, int t, int wave,
+                                           int lane, uint8_t* kd, uint8_t* vd) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int blk = wave * 4 + i;
+        const int row = 4 * blk + (lane >> 4);
+        const int off = (t * kBN + row) * (kHeadDim * 2) + 16 * ((lane & 15) ^ swz(row));
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, kd + blk * 1024, 16, off, 0, 0, 0);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, vd + blk * 1024, 16, off, 0, 0, 0);
+    }
+}
 
 // Map the 1-D workgroup id to (q tile, sequence, q head).  Groups of
 // 8*n_rep consecutive ids hold 8 (qtile, b, kv head) units x n_rep heads, laid
@@ -59,7 +101,7 @@ __device__ __forceinline__ bool map_block(int id, int n_qt, int B, int Hkv, int 
 }
 
 template <bool CAUSAL>
-__global__ __launch_bounds__(256) void prefill_bf16_kernel(
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void prefill_bf16_kernel(
     const bf16_t* __restrict__ q, const bf16_t* __restrict__ kc, const bf16_t* __restrict__ vc, int64_t cap,
     const int32_t* __restrict__ start_pos, int max_start, int S, int B, int Hq, int Hkv, float scale_log2,
     bf16_t* __restrict__ out) {
@@ -71,12 +113,19 @@ __global__ __launch_bounds__(256) void prefill_bf16_kernel(
     const int start = min(max(start_pos[b], 0), max_start);
     const int m0 = qt * kBM;
 
-    __shared__ __attribute__((aligned(16))) bf16_t k_lds[kBN * kKStride];
-    __shared__ __attribute__((aligned(16))) bf16_t vt_lds[kHeadDim * kVStride];
+    __shared__ __attribute__((aligned(1024))) uint8_t stage[2][2][kTileBytes];  // [buffer][K, V]
 
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
     const int n = lane & 31, hh = lane >> 5;
+
+    const int L = start + S;                                 // cache rows holding keys for this chunk
+    const int kend = CAUSAL ? min(start + m0 + kBM, L) : L;  // keys any row of the tile can see
+    const int n_tiles = (kend + kBN - 1) / kBN;
+    const int64_t head0 = ((int64_t)b * Hkv + kvh) * cap * kHeadDim;
+    const __amdgpu_buffer_rsrc_t rk = make_rsrc(kc + head0, L * kHeadDim * 2);
+    const __amdgpu_buffer_rsrc_t rv = make_rsrc(vc + head0, L * kHeadDim * 2);
+    issue_tile(rk, rv, 0, wave, lane, stage[0][0], stage[0][1]);
 
     // Q fragments (B operand of S^T = K Q^T): query row qrow, dims 16ks + 8hh .. +7.
     const int qrow = m0 + wave * 32 + n;
@@ -96,115 +145,90 @@ __global__ __launch_bounds__(256) void prefill_bf16_kernel(
 #pragma unroll
         for (int r = 0; r < 16; ++r) oacc[i][r] = 0.f;
     float m_run = -INFINITY, l_run = 0.f;
+    const int qpos = start + qrow;                      // absolute position of my query
+    const int wave_first = start + m0 + wave * 32;      // first position of this wave's rows
+    // transposed-read coordinates of this lane for the V^T fragments
+    const int vg = lane >> 4, vi = lane & 15;
+    const int v_h = vg >> 1;                            // key half of the A operand
+    const int v_col = 16 * (vg & 1) + 4 * (vi & 3);     // column inside a 32-dim block
 
-    const int L = start + S;                                     // keys in the cache for this chunk
-    const int kend = CAUSAL ? min(start + m0 + kBM, L) : L;      // keys any row of the tile can see
-    const int qpos = start + qrow;                               // absolute position of my query
-    const int wave_last = start + m0 + wave * 32 + 31;           // last position of this wave's rows
-    const bf16_t* Kg = kc + ((int64_t)b * Hkv + kvh) * cap * kHeadDim;
-    const bf16_t* Vg = vc + ((int64_t)b * Hkv + kvh) * cap * kHeadDim;
+    for (int t = 0; t < n_tiles; ++t) {
+        const int sb = t & 1;
+        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's copies of tile t have landed
+        __syncthreads();                     // ... and every wave's; tile t-1 is fully consumed
+        if (t + 1 < n_tiles) issue_tile(rk, rv, t + 1, wave, lane, stage[sb ^ 1][0], stage[sb ^ 1][1]);
+        const uint8_t* kt_lds = stage[sb][0];
+        const uint8_t* vt_lds = stage[sb][1];
+        const int kt = t * kBN;
+        if (CAUSAL && kt > wave_first + 31) continue;  // the whole tile is above this wave's diagonal
 
-    for (int kt = 0; kt < kend; kt += kBN) {
-        // ---- stage K tile [64 keys][128 dims] and V^T tile [128 dims][64 keys]
+        // ---- S^T = K Q^T for the 64 keys: two 32x32 blocks
+        f32x16_v sacc[2];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int p = tid + 256 * i;
-            const int key = p >> 4, ch = p & 15;
-            uint4 u = make_uint4(0, 0, 0, 0);
-            if (kt + key < kend) u = *reinterpret_cast<const uint4*>(Kg + (int64_t)(kt + key) * kHeadDim + 8 * ch);
-            *reinterpret_cast<uint4*>(&k_lds[key * kKStride + 8 * ch]) = u;
-        }
-        {
-            const int a = tid >> 4, ch = tid & 15;  // keys 4a..4a+3, dims 8ch..8ch+7
-            uint4 v[4];
+        for (int nb = 0; nb < 2; ++nb) {
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int key = kt + 4 * a + r;
-                v[r] = make_uint4(0, 0, 0, 0);
-                if (key < kend) v[r] = *reinterpret_cast<const uint4*>(Vg + (int64_t)key * kHeadDim + 8 * ch);
-            }
-            const uint32_t* w0 = reinterpret_cast<const uint32_t*>(&v[0]);
-            const uint32_t* w1 = reinterpret_cast<const uint32_t*>(&v[1]);
-            const uint32_t* w2 = reinterpret_cast<const uint32_t*>(&v[2]);
-            const uint32_t* w3 = reinterpret_cast<const uint32_t*>(&v[3]);
+            for (int r = 0; r < 16; ++r) sacc[nb][r] = 0.f;
+            const int row = nb * 32 + n;
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                // dim 8ch+2i (low halves) and 8ch+2i+1 (high halves) of the 4 keys
-                const uint2 lo = make_uint2((w0[i] & 0xffffu) | (w1[i] << 16), (w2[i] & 0xffffu) | (w3[i] << 16));
-                const uint2 hi = make_uint2((w0[i] >> 16) | (w1[i] & 0xffff0000u),
-                                            (w2[i] >> 16) | (w3[i] & 0xffff0000u));
-                *reinterpret_cast<uint2*>(&vt_lds[(8 * ch + 2 * i) * kVStride + 4 * a]) = lo;
-                *reinterpret_cast<uint2*>(&vt_lds[(8 * ch + 2 * i + 1) * kVStride + 4 * a]) = hi;
+            for (int ks = 0; ks < 8; ++ks) {
+                const uint4 ku =
+                    *reinterpret_cast<const uint4*>(kt_lds + row * 256 + 16 * ((2 * ks + hh) ^ swz(row)));
+                sacc[nb] = mfma32(as_bf16x8(ku), qf[ks], sacc[nb]);
             }
         }
-        __syncthreads();
-
-        const bool wave_active = !CAUSAL || kt <= wave_last;
-        if (wave_active) {
-            // ---- S^T = K Q^T for the 64 keys: two 32x32 blocks
-            f32x16_v sacc[2];
-#pragma unroll
-            for (int nb = 0; nb < 2; ++nb) {
-#pragma unroll
-                for (int r = 0; r < 16; ++r) sacc[nb][r] = 0.f;
-#pragma unroll
-                for (int ks = 0; ks < 8; ++ks) {
-                    const uint4 ku = *reinterpret_cast<const uint4*>(&k_lds[(nb * 32 + n) * kKStride + 16 * ks + 8 * hh]);
-                    sacc[nb] = mfma32(as_bf16x8(ku), qf[ks], sacc[nb]);
-                }
-            }
-            // ---- online softmax for query row n (keys: 8*(r/4) + 4*hh + r%4 of block nb)
-            const bool need_mask = kt + kBN > kend || (CAUSAL && kt + kBN - 1 > start + m0 + wave * 32);
-            float tmax = -INFINITY;
+        // ---- online softmax for query row n (keys 8*(r/4) + 4*hh + r%4 of block nb)
+        if (kt + kBN > kend || (CAUSAL && kt + kBN - 1 > wave_first)) {  // diagonal or last tile
 #pragma unroll
             for (int nb = 0; nb < 2; ++nb)
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
-                    float s = sacc[nb][r] * scale_log2;
-                    if (need_mask) {
-                        const int key = kt + nb * 32 + 8 * (r >> 2) + 4 * hh + (r & 3);
-                        if (key >= kend || (CAUSAL && key > qpos)) s = -INFINITY;
-                    }
-                    sacc[nb][r] = s;
-                    tmax = fmaxf(tmax, s);
+                    const int key = kt + nb * 32 + 8 * (r >> 2) + 4 * hh + (r & 3);
+                    if (key >= kend || (CAUSAL && key > qpos)) sacc[nb][r] = -INFINITY;
                 }
-            tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
-            const float m_new = fmaxf(m_run, tmax);
-            // m_new is finite: key 0 is visible to every query and tile 0 comes first
-            const float alpha = fast_exp2(m_run - m_new);
-            float psum = 0.f;
-            bf16x8_v pf[4];
+        }
+        float tmax = -INFINITY;
 #pragma unroll
-            for (int nb = 0; nb < 2; ++nb)
+        for (int nb = 0; nb < 2; ++nb)
 #pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    const float p = fast_exp2(sacc[nb][r] - m_new);
-                    psum += p;
-                    pf[nb * 2 + (r >> 3)][r & 7] = (__bf16)p;
-                }
-            psum += __shfl_xor(psum, 32);
-            l_run = l_run * alpha + psum;
-            m_run = m_new;
+            for (int r = 0; r < 16; ++r) tmax = fmaxf(tmax, sacc[nb][r]);
+        tmax = fmaxf(tmax, __shfl_xor(tmax, 32)) * scale_log2;  // raw-score max; the scale is positive
+        const float m_new = fmaxf(m_run, tmax);
+        const float alpha = fast_exp2(m_run - m_new);  // 0 on the first tile (m_run = -inf)
+        m_run = m_new;  // finite: key 0 is visible to every query and tile 0 comes first
+        const float neg_m = -m_new;
+        float psum = 0.f;
+        bf16x8_v pf[4];
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
+        for (int nb = 0; nb < 2; ++nb)
 #pragma unroll
-                for (int r = 0; r < 16; ++r) oacc[i][r] *= alpha;
-            // ---- O^T += V^T P^T: 4 dim blocks x 4 key steps of 16
+            for (int r = 0; r < 16; ++r) {
+                const float p = fast_exp2(__builtin_fmaf(sacc[nb][r], scale_log2, neg_m));
+                psum += p;
+                pf[nb * 2 + (r >> 3)][r & 7] = (__bf16)p;
+            }
+        l_run = l_run * alpha + psum;
 #pragma unroll
-            for (int t = 0; t < 4; ++t) {
+        for (int i = 0; i < 4; ++i)
 #pragma unroll
-                for (int db = 0; db < 4; ++db) {
-                    const bf16_t* vp = &vt_lds[(db * 32 + n) * kVStride + 16 * t + 4 * hh];
-                    const uint2 lo = *reinterpret_cast<const uint2*>(vp);
-                    const uint2 hi = *reinterpret_cast<const uint2*>(vp + 8);
-                    const uint4 vu = make_uint4(lo.x, lo.y, hi.x, hi.y);
-                    oacc[db] = mfma32(as_bf16x8(vu), pf[t], oacc[db]);
-                }
+            for (int r = 0; r < 16; ++r) oacc[i][r] *= alpha;
+        // ---- O^T += V^T P^T: 4 dim blocks x 4 key steps of 16; the A operand
+        // (dims x keys) comes straight from the row-major V tile by transposed reads
+#pragma unroll
+        for (int st = 0; st < 4; ++st) {
+            const int r0 = 16 * st + 4 * v_h + (vi >> 2);  // keys of slots 0..3; slots 4..7 are 8 rows on
+            const int r1 = r0 + 8;
+#pragma unroll
+            for (int db = 0; db < 4; ++db) {
+                const int col = 32 * db + v_col;
+                const uint2 lo = read_tr16(vt_lds + r0 * 256 + 16 * ((col >> 3) ^ swz(r0)) + 2 * (col & 7));
+                const uint2 hi = read_tr16(vt_lds + r1 * 256 + 16 * ((col >> 3) ^ swz(r1)) + 2 * (col & 7));
+                const uint4 vu = make_uint4(lo.x, lo.y, hi.x, hi.y);
+                oacc[db] = mfma32(as_bf16x8(vu), pf[st], oacc[db]);
             }
         }
-        __syncthreads();
     }
 
+    l_run += __shfl_xor(l_run, 32);  // the two lane halves hold different keys of the row
     if (qrow < S) {
         const float inv = 1.0f / l_run;
         bf16_t* op = out + (((int64_t)b * S + qrow) * Hq + hq) * kHeadDim;
