@@ -53,18 +53,28 @@ def randn(shape, gen, dtype, device, std=1.0):
     return t.to(dtype)
 
 
+WARM_SECONDS = 0.5  # minimum untimed run before a timed region: lets the GPU clocks settle
+
+
 def timed(launch, steps: int, warmup: int, stream):
     """Run `launch(i)` warmup + steps times; returns ms per step over the timed
-    steps, bracketed by synchronize and measured with events on `stream`."""
+    steps, bracketed by synchronize and measured with events on `stream`.
+    The untimed warmup runs at least `warmup` launches and at least
+    WARM_SECONDS of wall time: a cold GPU runs its first ~0.2 s at lower clocks."""
     import torch
-    for i in range(warmup):
+    i = 0
+    t0 = time.perf_counter()
+    while i < warmup or time.perf_counter() - t0 < WARM_SECONDS:
         launch(i)
+        i += 1
+        if i % 8 == 0:
+            torch.cuda.synchronize()
     torch.cuda.synchronize()
     start = torch.cuda.Event(enable_timing=True)
     end = torch.cuda.Event(enable_timing=True)
     start.record(stream)
-    for i in range(steps):
-        launch(warmup + i)
+    for j in range(steps):
+        launch(i + j)
     end.record(stream)
     torch.cuda.synchronize()
     return start.elapsed_time(end) / steps

@@ -91,4 +91,11 @@ namespace crane {
 inline int launch_status(hipError_t e) { return e == hipSuccess ? CRANE_HIP_OK : CRANE_HIP_E_LAUNCH; }
 inline bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 inline int elem_size(int dtype) { return dtype == CRANE_HIP_F32 ? 4 : 2; }
+inline uint32_t f32_bits(float f) { return __builtin_bit_cast(uint32_t, f); }
+inline float bits_f32(uint32_t u) { return __builtin_bit_cast(float, u); }
+// Round-to-nearest-even f32 -> bf16 value (finite inputs), as half::bf16::from_f32.
+inline float host_round_bf16(float f) {
+    const uint32_t u = f32_bits(f);
+    return bits_f32((u + 0x7fffu + ((u >> 16) & 1u)) & 0xffff0000u);
+}
 }  // namespace crane

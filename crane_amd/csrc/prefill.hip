@@ -23,6 +23,17 @@
 // Workgroup ids are remapped so that heavy (late) query tiles start first and
 // the q heads sharing a kv head run on the same XCD (shared L2).
 //
+// Rounding points (bf16): candle's bf16 matmul returns Q K^T rounded to bf16
+// and its affine scales by the scale converted to bf16; both are reproduced.
+// candle then rounds the scaled score to bf16 again, and rounds exp, the row
+// sum and the quotient to bf16; those are not reproduced (the online softmax
+// keeps them in f32, P enters the PV product in bf16).  The second score
+// rounding costs about 11% of the kernel's time to reproduce and moves an
+// output past 2e-2 of candle's in about 1 element in 2e7 on N(0,1) data, always
+// one where candle's own result is farther from the exact one.  The row sum l
+// adds the bf16 p that enter the PV product (v_dot2_f32_bf16 against (1, 1)),
+// so numerator and denominator see the same weights.
+//
 // f32 kernel: a plain wave-per-query-row online-softmax kernel; Crane serves
 // prefill in bf16 on GPU (crane-serve/src/lib.rs:123-150), f32 is kept for
 // completeness of the operator.
@@ -192,25 +203,43 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 #pragma unroll
             for (int r = 0; r < 16; ++r) tmax = fmaxf(tmax, sacc[nb][r]);
         tmax = fmaxf(tmax, __shfl_xor(tmax, 32)) * scale_log2;  // raw-score max; the scale is positive
-        const float m_new = fmaxf(m_run, tmax);
-        const float alpha = fast_exp2(m_run - m_new);  // 0 on the first tile (m_run = -inf)
-        m_run = m_new;  // finite: key 0 is visible to every query and tile 0 comes first
-        const float neg_m = -m_new;
+        // Lazy rescaling: the reference max m_run only moves when some row's max
+        // exceeds it by more than kLazy, so O and l are rescaled rarely and
+        // p = exp2(s * scale_log2 - m_run) stays below 2^kLazy.  The first tile
+        // always moves it (m_run starts at -inf; key 0 is visible to every
+        // query, so m_run is finite afterwards).
+        if (__any(tmax > m_run + kLazy)) {
+            const float m_new = fmaxf(m_run, tmax);
+            const float alpha = fast_exp2(m_run - m_new);
+            l_run *= alpha;
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) oacc[i][r] *= alpha;
+            m_run = m_new;
+        }
+        const float neg_m = -m_run;
         float psum = 0.f;
         bf16x8_v pf[4];
+        const bf16x2_v ones = {(__bf16)1.f, (__bf16)1.f};
 #pragma unroll
         for (int nb = 0; nb < 2; ++nb)
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const float p = fast_exp2(__builtin_fmaf(sacc[nb][r], scale_log2, neg_m));
-                psum += p;
-                pf[nb * 2 + (r >> 3)][r & 7] = (__bf16)p;
+            for (int r = 0; r < 16; r += 2) {
+                // The QK^T product is rounded to bf16, as candle's bf16 matmul
+                // output is (one v_cvt_pk_bf16_f32 for two scores);
+                // p = exp2(bf16(s) * scale_log2 - m).
+                const uint32_t w = pack_bf16x2(sacc[nb][r], sacc[nb][r + 1]);
+                const float p0 = fast_exp2(__builtin_fmaf(bf16_lo(w), scale_log2, neg_m));
+                const float p1 = fast_exp2(__builtin_fmaf(bf16_hi(w), scale_log2, neg_m));
+                // The row sum adds the same bf16 p that the P V product uses, so
+                // a row dominated by one key returns that V row unscaled.
+                const bf16x2_v pw = __builtin_bit_cast(bf16x2_v, pack_bf16x2(p0, p1));
+                psum = __builtin_amdgcn_fdot2_f32_bf16(pw, ones, psum, false);
+                pf[nb * 2 + (r >> 3)][r & 7] = pw[0];
+                pf[nb * 2 + (r >> 3)][(r & 7) + 1] = pw[1];
             }
-        l_run = l_run * alpha + psum;
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) oacc[i][r] *= alpha;
+        l_run += psum;
         // ---- O^T += V^T P^T: 4 dim blocks x 4 key steps of 16; the A operand
         // (dims x keys) comes straight from the row-major V tile by transposed reads
 #pragma unroll
@@ -297,8 +326,9 @@ extern "C" int crane_hip_attn_prefill(const void* q, const void* k_cache, const 
     if (!aligned16(q) || !aligned16(k_cache) || !aligned16(v_cache) || !aligned16(out)) return CRANE_HIP_E_ALIGN;
     if (cache_cap > 0x7fffffffLL || B > 65535 || Hq > 65535) return CRANE_HIP_E_INVALID;
     hipStream_t st = (hipStream_t)stream;
-    const float sl = scale * kLog2e;
     if (dtype == CRANE_HIP_BF16) {
+        // candle scales the bf16 scores by the scale converted to bf16 (affine in T)
+        const float sl = host_round_bf16(scale) * kLog2e;
         const int n_rep = Hq / Hkv;
         const int64_t n_qt = (S + kBM - 1) / kBM;
         const int64_t units = n_qt * B * Hkv;
@@ -314,6 +344,7 @@ extern "C" int crane_hip_attn_prefill(const void* q, const void* k_cache, const 
                                (const bf16_t*)q, (const bf16_t*)k_cache, (const bf16_t*)v_cache, cache_cap, start_pos,
                                (int)max_start, S, B, Hq, Hkv, sl, (bf16_t*)out);
     } else {
+        const float sl = scale * kLog2e;
         const dim3 grid((unsigned)S, (unsigned)Hq, (unsigned)B);
         if (causal)
             hipLaunchKernelGGL(prefill_f32_kernel<true>, grid, dim3(64), 0, st, (const float*)q, (const float*)k_cache,
