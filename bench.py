@@ -80,6 +80,38 @@ def timed(launch, steps: int, warmup: int, stream):
     return start.elapsed_time(end) / steps
 
 
+TRAFFIC_FILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "hbm_traffic_pmc.md")
+
+
+def pmc_traffic():
+    """HBM bytes per launch measured with rocprofv3 FETCH_SIZE / WRITE_SIZE
+    (scaled by a calibration kernel of known traffic) for each workload, from
+    the TRAFFIC lines of the committed counter summary; {} if absent."""
+    out = {}
+    try:
+        for line in open(TRAFFIC_FILE):
+            f = line.split()
+            if len(f) == 3 and f[0] == "TRAFFIC":
+                out[f[1]] = int(f[2])
+    except OSError:
+        pass
+    return out
+
+
+def launch_percentiles(launch, n: int, stream, first: int = 0):
+    """Per-launch times (events around each launch, on `stream`) over n
+    launches after the timed region: [p10, p50, p90] in ms."""
+    import torch
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(n)]
+    for j, (a, b) in enumerate(evs):
+        a.record(stream)
+        launch(first + j)
+        b.record(stream)
+    torch.cuda.synchronize()
+    t = np.array([a.elapsed_time(b) for a, b in evs])
+    return [round(float(x), 5) for x in np.percentile(t, [10, 50, 90])]
+
+
 def cpu_info():
     threads = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or len(os.sched_getaffinity(0))
     model = "unknown"
@@ -123,12 +155,13 @@ def bench_decode(args, dev, stream, lib):
             raise RuntimeError(f"crane_hip_attn_decode failed: {rc}")
 
     ms = timed(launch, args.steps, args.warmup, stream)
+    pct = launch_percentiles(launch, 100, stream)
     kv_bytes = int(kv_len.sum()) * Hkv * D * 2 * 2
     algo_bytes = kv_bytes + 2 * B * Hq * D * 2
     gbs = algo_bytes / (ms * 1e-3) / 1e9
     log(f"[decode c3] {ms * 1e3:.2f} us/step, {gbs:.1f} GB/s algorithmic ({gbs / HBM_PEAK_GBS * 100:.1f}% of HBM)")
     data = dict(ms=ms, gbs=gbs, algo_bytes=algo_bytes, kv_bytes=kv_bytes, lens=lens, kv_len=kv_len,
-                B=B, Hq=Hq, Hkv=Hkv, cap=cap)
+                B=B, Hq=Hq, Hkv=Hkv, cap=cap, pct=pct)
     data["_tensors"] = (q, ks[0], vs[0], kv_len)
     return data
 
@@ -188,10 +221,11 @@ def bench_prefill(args, dev, stream, lib):
             raise RuntimeError(f"crane_hip_attn_prefill failed: {rc}")
 
     ms = timed(launch, max(3, args.steps // 2), max(2, args.warmup // 2), stream)
+    pct = launch_percentiles(launch, 100, stream)
     flops = 4.0 * D * Hq * B * S * (S + 1) / 2
     tflops = flops / (ms * 1e-3) / 1e12
     log(f"[prefill c4] {ms:.3f} ms/step, {tflops:.1f} TFLOP/s ({tflops / BF16_PEAK_TFLOPS * 100:.1f}% of bf16 peak)")
-    return dict(ms=ms, tflops=tflops, flops=flops, B=B, S=S, Hq=Hq, Hkv=Hkv, _tensors=(q, k, v))
+    return dict(ms=ms, tflops=tflops, flops=flops, B=B, S=S, Hq=Hq, Hkv=Hkv, pct=pct, _tensors=(q, k, v))
 
 
 def bench_prefill_c2(args, dev, stream, lib):
@@ -264,51 +298,84 @@ def bench_append(args, dev, stream, lib):
 
 # ----------------------------------------------------------- CPU baseline
 
+def _timed_runs(fn, min_seconds: float, min_runs: int):
+    """Run fn() until both min_runs runs and min_seconds of wall time are done;
+    returns the list of per-run seconds."""
+    times = []
+    t_end = time.perf_counter() + min_seconds
+    while len(times) < min_runs or time.perf_counter() < t_end:
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return times
+
+
 def cpu_baseline(dec, pre):
     """The oracle (C restatement of Crane's candle-CPU path, bf16 rounding
-    points) on the host cores, on bounded samples of configs 3 and 4."""
-    import torch
+    points) on the host cores, on bounded samples of configs 3 and 4: the full
+    config-3 step repeated for >= 10 s (median run), config 4 sequence by
+    sequence for >= 10 s, and 1-thread samples of each."""
     sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
     import oracle
     threads, model = cpu_info()
     res = {}
+    scale = 1.0 / math.sqrt(D)
     if dec is not None:
         q, k, v, kv_len = dec["_tensors"]
-        nb = 8                                             # first 8 of the 32 sequences
-        qn = q[:nb].float().cpu().numpy()
-        kn = np.ascontiguousarray(k[:nb].float().cpu().numpy())
-        vn = np.ascontiguousarray(v[:nb].float().cpu().numpy())
-        lens = np.ascontiguousarray(kv_len[:nb])
-        times = []
-        t_end = time.time() + 15.0
-        while len(times) < 5 and (time.time() < t_end or not times):
-            t0 = time.perf_counter()
-            oracle.attn_decode(qn, kn, vn, lens, 1.0 / math.sqrt(D), "bf16", oracle.DECODE_GROUPED, threads)
-            times.append(time.perf_counter() - t0)
+        qn = q.float().cpu().numpy()
+        kn = np.ascontiguousarray(k.float().cpu().numpy())
+        vn = np.ascontiguousarray(v.float().cpu().numpy())
+        lens = np.ascontiguousarray(kv_len)
+        B = qn.shape[0]
+
+        def step(nb, nt):
+            return lambda: oracle.attn_decode(qn[:nb], kn[:nb], vn[:nb], lens[:nb], scale, "bf16",
+                                              oracle.DECODE_GROUPED, nt)
+
+        def nbytes(nb):
+            return int(lens[:nb].sum()) * dec["Hkv"] * D * 2 * 2 + 2 * nb * dec["Hq"] * D * 2
+
+        times = _timed_runs(step(B, threads), 10.0, 5)
         t = float(np.median(times))
-        nbytes = int(lens.sum()) * dec["Hkv"] * D * 2 * 2 + 2 * nb * dec["Hq"] * D * 2
-        res["decode"] = dict(value=nbytes / t / 1e9, unit="GB/s", cores=threads, kind="port",
-                             sample=f"config 3, sequences 0-7 of 32 (sum L={int(lens.sum())}), bf16 op chain, "
-                                    f"median of {len(times)} runs, {t * 1e3:.1f} ms each; host {model}")
-        log(f"[cpu decode] {res['decode']['value']:.2f} GB/s on {threads} threads")
+        t1 = float(np.median(_timed_runs(step(4, 1), 3.0, 3)))
+        res["decode"] = dict(value=nbytes(B) / t / 1e9, unit="GB/s", cores=threads, kind="port",
+                             one_thread=round(nbytes(4) / t1 / 1e9, 3),
+                             sample=f"the full config-3 step (32 sequences, sum L={int(lens.sum())}), bf16 op chain, "
+                                    f"median of {len(times)} runs ({sum(times):.1f} s, {t * 1e3:.1f} ms each); "
+                                    f"one_thread: sequences 0-3 on 1 thread; host {model}")
+        log(f"[cpu decode] {res['decode']['value']:.2f} GB/s on {threads} threads "
+            f"({res['decode']['one_thread']:.2f} GB/s on 1)")
     if pre is not None:
         q, k, v = pre["_tensors"]
-        S, Hq = pre["S"], pre["Hq"]
-        qn = np.ascontiguousarray(q[:1].float().cpu().numpy())
-        kn = np.ascontiguousarray(k[:1].float().cpu().numpy())
-        vn = np.ascontiguousarray(v[:1].float().cpu().numpy())
-        rows = [(S - 16, S)]                                # 16 heaviest rows, all heads of sequence 0
+        B, S, Hq = pre["B"], pre["S"], pre["Hq"]
+        start = np.zeros(1, np.int32)
+
+        def seq_flops(r0, r1):
+            return 4.0 * D * Hq * (r1 * (r1 + 1) - r0 * (r0 + 1)) / 2
+
+        flops, t, done = 0.0, 0.0, 0
+        for b in range(B):
+            qn = np.ascontiguousarray(q[b:b + 1].float().cpu().numpy())
+            kn = np.ascontiguousarray(k[b:b + 1].float().cpu().numpy())
+            vn = np.ascontiguousarray(v[b:b + 1].float().cpu().numpy())
+            t0 = time.perf_counter()
+            oracle.attn_prefill(qn, kn, vn, start, scale, True, "bf16", nthreads=threads)
+            t += time.perf_counter() - t0
+            flops += seq_flops(0, S)
+            done += 1
+            if t >= 10.0:
+                break
+        r0 = S - 64                                           # 1 thread: the 64 heaviest rows of sequence 0
         t0 = time.perf_counter()
-        flops = 0.0
-        for r0, r1 in rows:
-            oracle.attn_prefill(qn, kn, vn, np.zeros(1, np.int32), 1.0 / math.sqrt(D), True, "bf16",
-                                rows=(r0, r1), nthreads=threads)
-            flops += sum(4.0 * D * (i + 1) for i in range(r0, r1)) * Hq
-        t = time.perf_counter() - t0
+        oracle.attn_prefill(qn, kn, vn, start, scale, True, "bf16", rows=(r0, S), nthreads=1)
+        t1 = time.perf_counter() - t0
         res["prefill"] = dict(value=flops / t / 1e12, unit="TFLOP/s", cores=threads, kind="port",
-                              sample=f"config 4, sequence 0, rows {rows[0][0]}-{rows[0][1] - 1} x {Hq} heads "
-                                     f"(causal flops counted), bf16 op chain, {t:.1f} s; host {model}")
-        log(f"[cpu prefill] {res['prefill']['value'] * 1e3:.3f} GFLOP/s on {threads} threads")
+                              one_thread=round(seq_flops(r0, S) / t1 / 1e12, 5),
+                              sample=f"config 4, {done} of {B} sequences (all {S} rows x {Hq} heads, causal flops "
+                                     f"counted), bf16 op chain, {t:.1f} s; one_thread: rows {r0}-{S - 1} of the last "
+                                     f"sequence run, {t1:.1f} s; host {model}")
+        log(f"[cpu prefill] {res['prefill']['value'] * 1e3:.3f} GFLOP/s on {threads} threads "
+            f"({res['prefill']['one_thread'] * 1e3:.3f} on 1)")
     return res
 
 
@@ -320,7 +387,7 @@ def main():
     ap.add_argument("--only", choices=["decode", "prefill", "append", "all"], default="all")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true",
-                    help="also run a plain 1 GiB device-to-device copy (for scaling FETCH_SIZE/WRITE_SIZE counters)")
+                    help="also run a plain elementwise kernel over 1 GiB (scales FETCH_SIZE/WRITE_SIZE counters)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: the attention path runs on a single MI355X and this build "
@@ -340,13 +407,13 @@ def main():
     log(f"device: {torch.cuda.get_device_name(dev)}; lib: {_lib.version()}")
 
     if args.copy_calibration:
-        import torch
-        src = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
+        # A plain elementwise kernel of known traffic: reads 1 GiB, writes 1 GiB.
+        src = torch.ones(1 << 28, dtype=torch.float32, device=dev)
         dst = torch.empty_like(src)
         for _ in range(3):
-            dst.copy_(src)
+            torch.neg(src, out=dst)
         torch.cuda.synchronize()
-        log("[calibration] 3 copies of 1 GiB (1073741824 B read + written each)")
+        log("[calibration] 3 x neg over 2^28 f32 (1073741824 B read + 1073741824 B written each)")
         del src, dst
         torch.cuda.empty_cache()
     dec = pre = c5 = c2 = app = None
@@ -362,6 +429,8 @@ def main():
         app = bench_append(args, dev, stream, lib)
     cpu = {} if args.no_cpu_baseline else cpu_baseline(dec, pre)
 
+    traffic = pmc_traffic()
+    src = os.path.relpath(TRAFFIC_FILE, os.path.dirname(os.path.abspath(__file__)))
     line = {"metric": METRIC, "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
             "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
             "data": "synthetic (seeded N(0,1) q/K/V; lengths U{512..4096} seeded)"}
@@ -373,16 +442,21 @@ def main():
                        "batch": 32, "q_heads": 32, "kv_heads": 8, "head_dim": 128,
                        "sum_kv_rows": int(dec["kv_len"].sum()), "kv_bytes_per_step": dec["kv_bytes"]},
             "roofline": {"bound": "hbm", "achieved": round(dec["gbs"], 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                         "frac": round(dec["gbs"] / HBM_PEAK_GBS, 4), "traffic": None,
-                         "kernel": "decode_split_kernel<bf16,4>", "algo_bytes_per_launch": dec["algo_bytes"]},
+                         "frac": round(dec["gbs"] / HBM_PEAK_GBS, 4), "traffic": traffic.get("decode_c3"),
+                         "traffic_source": src,
+                         "kernel": "decode_chunk_kernel + decode_merge_kernel (one crane_hip_attn_decode call)",
+                         "algo_bytes_per_launch": dec["algo_bytes"]},
+            "ms_p10_p50_p90": dec["pct"],
         })
     if pre is not None:
         pre_obj = {"metric": "prefill attn TFLOP/s (c4: Qwen2.5-7B shape, B=8, S=4096, 28/4 heads, causal, bf16)",
                    "value": round(pre["tflops"], 2), "unit": "TFLOP/s", "ms_per_step": round(pre["ms"], 4),
                    "roofline": {"bound": "mfma", "achieved": round(pre["tflops"], 2), "peak": BF16_PEAK_TFLOPS,
                                 "unit": "TFLOP/s", "frac": round(pre["tflops"] / BF16_PEAK_TFLOPS, 4),
-                                "traffic": None, "kernel": "prefill_bf16_kernel<causal>",
-                                "algo_flops_per_launch": pre["flops"]}}
+                                "traffic": traffic.get("prefill_c4"), "traffic_source": src,
+                                "kernel": "prefill_bf16_kernel<true>",
+                                "algo_flops_per_launch": pre["flops"]},
+                   "ms_p10_p50_p90": pre["pct"]}
         if "prefill" in cpu:
             pre_obj["cpu_baseline"] = cpu["prefill"]
         if dec is None:
