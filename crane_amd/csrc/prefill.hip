@@ -75,20 +75,39 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, in
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, bytes, 0x00020000);
 }
 
-// Copy keys [64 t, 64 t + 64) of K and V into one LDS stage with
+// Copy keys [64 t, 64 t + 64) of K (or V) into one 16 KiB LDS buffer with
 // bounds-checked buffer_load ... lds (rows past the cache rows read as zero).
-// Wave w copies the 1 KiB blocks 4w..4w+3 of each tile; lane l of block blk
+// Wave w copies the 1 KiB blocks 4w..4w+3 of the tile; lane l of block blk
 // fills row 4 blk + l/16, chunk l%16, with global chunk (l%16) ^ swz(row).
-__device__ __forceinline__ void issue_tile(__amdgpu_buffer_rsrc_t rk, __amdgpu_buffer_rsrc_t rv, int t, int wave,
-                                           int lane, uint8_t* kd, uint8_t* vd) {
+__device__ __forceinline__ void issue_tile(__amdgpu_buffer_rsrc_t rsrc, int t, int wave, int lane, uint8_t* dst) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const int blk = wave * 4 + i;
         const int row = 4 * blk + (lane >> 4);
         const int off = (t * kBN + row) * (kHeadDim * 2) + 16 * ((lane & 15) ^ swz(row));
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, kd + blk * 1024, 16, off, 0, 0, 0);
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, vd + blk * 1024, 16, off, 0, 0, 0);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, dst + blk * 1024, 16, off, 0, 0, 0);
     }
+}
+
+// s_waitcnt with only vmcnt constrained (expcnt and lgkmcnt at their maxima).
+#define CRANE_WAIT_VMCNT(n) __builtin_amdgcn_s_waitcnt(0x0F70 | ((n) & 15) | (((n) >> 4) << 14))
+
+// S^T = K Q^T for the 64 keys of a tile: two 32x32 blocks of 8 MFMAs each.
+// Lane (n, hh) holds keys nb*32 + 8*(r/4) + 4*hh + r%4 of query row n in s[nb][r].
+__device__ __forceinline__ void qk_tile(const uint8_t* kt_lds, const bf16x8_v (&qf)[8], int n, int hh,
+                                        f32x16_v (&s)[2]) {
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) s[nb][r] = 0.f;
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks)
+#pragma unroll
+        for (int nb = 0; nb < 2; ++nb) {
+            const int row = nb * 32 + n;
+            const uint4 ku = *reinterpret_cast<const uint4*>(kt_lds + row * 256 + 16 * ((2 * ks + hh) ^ swz(row)));
+            s[nb] = mfma32(as_bf16x8(ku), qf[ks], s[nb]);
+        }
 }
 
 // Map the 1-D workgroup id to (q tile, sequence, q head).  Groups of
@@ -124,7 +143,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     const int start = min(max(start_pos[b], 0), max_start);
     const int m0 = qt * kBM;
 
-    __shared__ __attribute__((aligned(1024))) uint8_t stage[2][2][kTileBytes];  // [buffer][K, V]
+    // K tiles t and t+1 and V tile t are resident while tile t is computed;
+    // K(t+2) and V(t+1) are in flight.
+    __shared__ __attribute__((aligned(1024))) uint8_t kbuf[2][kTileBytes];
+    __shared__ __attribute__((aligned(1024))) uint8_t vbuf[2][kTileBytes];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
@@ -136,7 +158,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     const int64_t head0 = ((int64_t)b * Hkv + kvh) * cap * kHeadDim;
     const __amdgpu_buffer_rsrc_t rk = make_rsrc(kc + head0, L * kHeadDim * 2);
     const __amdgpu_buffer_rsrc_t rv = make_rsrc(vc + head0, L * kHeadDim * 2);
-    issue_tile(rk, rv, 0, wave, lane, stage[0][0], stage[0][1]);
+    issue_tile(rk, 0, wave, lane, kbuf[0]);
+    issue_tile(rv, 0, wave, lane, vbuf[0]);
+    if (n_tiles > 1) issue_tile(rk, 1, wave, lane, kbuf[1]);
 
     // Q fragments (B operand of S^T = K Q^T): query row qrow, dims 16ks + 8hh .. +7.
     const int qrow = m0 + wave * 32 + n;
@@ -162,54 +186,48 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     const int vg = lane >> 4, vi = lane & 15;
     const int v_h = vg >> 1;                            // key half of the A operand
     const int v_col = 16 * (vg & 1) + 4 * (vi & 3);     // column inside a 32-dim block
+    const bf16x2_v ones = {(__bf16)1.f, (__bf16)1.f};
 
-    for (int t = 0; t < n_tiles; ++t) {
-        const int sb = t & 1;
-        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's copies of tile t have landed
-        __syncthreads();                     // ... and every wave's; tile t-1 is fully consumed
-        if (t + 1 < n_tiles) issue_tile(rk, rv, t + 1, wave, lane, stage[sb ^ 1][0], stage[sb ^ 1][1]);
-        const uint8_t* kt_lds = stage[sb][0];
-        const uint8_t* vt_lds = stage[sb][1];
+    // Tile 0 is visible to every row (key 0 precedes every query position).
+    if (n_tiles > 1) CRANE_WAIT_VMCNT(8); else CRANE_WAIT_VMCNT(4);  // this wave's K(0) copies
+    __syncthreads();                                                   // ... and every wave's
+    f32x16_v sa[2], sb[2];
+    qk_tile(kbuf[0], qf, n, hh, sa);
+
+    // One tile: softmax of tile t's scores (sc), S^T of tile t+1 (into sn),
+    // then O^T += V^T P^T for tile t.  The exp work of tile t and the MFMAs of
+    // tile t+1 are independent, so one wave keeps both pipes busy.
+    auto step = [&](int t, f32x16_v (&sc)[2], f32x16_v (&sn)[2]) {
+        CRANE_WAIT_VMCNT(0);  // this wave's copies of V(t) and K(t+1) have landed
+        __syncthreads();      // ... and every wave's; K(t) and V(t-1) are fully consumed
+        if (t + 2 < n_tiles) issue_tile(rk, t + 2, wave, lane, kbuf[t & 1]);
+        if (t + 1 < n_tiles) issue_tile(rv, t + 1, wave, lane, vbuf[(t + 1) & 1]);
         const int kt = t * kBN;
-        if (CAUSAL && kt > wave_first + 31) continue;  // the whole tile is above this wave's diagonal
-
-        // ---- S^T = K Q^T for the 64 keys: two 32x32 blocks
-        f32x16_v sacc[2];
-#pragma unroll
-        for (int nb = 0; nb < 2; ++nb) {
-#pragma unroll
-            for (int r = 0; r < 16; ++r) sacc[nb][r] = 0.f;
-            const int row = nb * 32 + n;
-#pragma unroll
-            for (int ks = 0; ks < 8; ++ks) {
-                const uint4 ku =
-                    *reinterpret_cast<const uint4*>(kt_lds + row * 256 + 16 * ((2 * ks + hh) ^ swz(row)));
-                sacc[nb] = mfma32(as_bf16x8(ku), qf[ks], sacc[nb]);
-            }
-        }
-        // ---- online softmax for query row n (keys 8*(r/4) + 4*hh + r%4 of block nb)
+        if (CAUSAL && kt > wave_first + 31) return;  // the whole tile is above this wave's diagonal
         if (kt + kBN > kend || (CAUSAL && kt + kBN - 1 > wave_first)) {  // diagonal or last tile
 #pragma unroll
             for (int nb = 0; nb < 2; ++nb)
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
                     const int key = kt + nb * 32 + 8 * (r >> 2) + 4 * hh + (r & 3);
-                    if (key >= kend || (CAUSAL && key > qpos)) sacc[nb][r] = -INFINITY;
+                    if (key >= kend || (CAUSAL && key > qpos)) sc[nb][r] = -INFINITY;
                 }
         }
         float tmax = -INFINITY;
 #pragma unroll
         for (int nb = 0; nb < 2; ++nb)
 #pragma unroll
-            for (int r = 0; r < 16; ++r) tmax = fmaxf(tmax, sacc[nb][r]);
-        tmax = fmaxf(tmax, __shfl_xor(tmax, 32)) * scale_log2;  // raw-score max; the scale is positive
+            for (int r = 0; r < 16; ++r) tmax = fmaxf(tmax, sc[nb][r]);
+        tmax *= scale_log2;  // this lane half's raw-score max; the scale is positive
         // Lazy rescaling: the reference max m_run only moves when some row's max
         // exceeds it by more than kLazy, so O and l are rescaled rarely and
-        // p = exp2(s * scale_log2 - m_run) stays below 2^kLazy.  The first tile
-        // always moves it (m_run starts at -inf; key 0 is visible to every
-        // query, so m_run is finite afterwards).
+        // p = exp2(s * scale_log2 - m_run) stays below 2^kLazy.  The decision is
+        // wave-wide, so each lane half's own max decides it; the row max over
+        // both halves (the two halves of a row share m_run) is only needed when
+        // m_run moves.  The first tile always moves it (m_run starts at -inf;
+        // key 0 is visible to every query, so m_run is finite afterwards).
         if (__any(tmax > m_run + kLazy)) {
-            const float m_new = fmaxf(m_run, tmax);
+            const float m_new = fmaxf(m_run, fmaxf(tmax, __shfl_xor(tmax, 32)));
             const float alpha = fast_exp2(m_run - m_new);
             l_run *= alpha;
 #pragma unroll
@@ -221,7 +239,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         const float neg_m = -m_run;
         float psum = 0.f;
         bf16x8_v pf[4];
-        const bf16x2_v ones = {(__bf16)1.f, (__bf16)1.f};
 #pragma unroll
         for (int nb = 0; nb < 2; ++nb)
 #pragma unroll
@@ -229,8 +246,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
                 // The QK^T product is rounded to bf16, as candle's bf16 matmul
                 // output is (one v_cvt_pk_bf16_f32 for two scores);
                 // p = exp2(bf16(s) * scale_log2 - m).
-                const uint32_t w = pack_bf16x2(sacc[nb][r], sacc[nb][r + 1]);
-                const float p0 = fast_exp2(__builtin_fmaf(bf16_lo(w), scale_log2, neg_m));
+                const uint32_t w = pack_bf16x2(sc[nb][r], sc[nb][r + 1]);
+                // low half moved up by v_perm (kept opaque, so the pair stays one cvt)
+                const float s0 = __uint_as_float(__builtin_amdgcn_perm(0u, w, 0x01000c0cu));
+                const float p0 = fast_exp2(__builtin_fmaf(s0, scale_log2, neg_m));
                 const float p1 = fast_exp2(__builtin_fmaf(bf16_hi(w), scale_log2, neg_m));
                 // The row sum adds the same bf16 p that the P V product uses, so
                 // a row dominated by one key returns that V row unscaled.
@@ -240,8 +259,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
                 pf[nb * 2 + (r >> 3)][(r & 7) + 1] = pw[1];
             }
         l_run += psum;
+        // Unconditional, so this stays in one basic block with the exp work
+        // above: past the last tile (or above this wave's diagonal) the
+        // result is simply not used, and nothing is in flight into that buffer.
+        qk_tile(kbuf[(t + 1) & 1], qf, n, hh, sn);
         // ---- O^T += V^T P^T: 4 dim blocks x 4 key steps of 16; the A operand
         // (dims x keys) comes straight from the row-major V tile by transposed reads
+        const uint8_t* vt_lds = vbuf[t & 1];
 #pragma unroll
         for (int st = 0; st < 4; ++st) {
             const int r0 = 16 * st + 4 * v_h + (vi >> 2);  // keys of slots 0..3; slots 4..7 are 8 rows on
@@ -255,6 +279,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
                 oacc[db] = mfma32(as_bf16x8(vu), pf[st], oacc[db]);
             }
         }
+    };
+    for (int t = 0; t < n_tiles; t += 2) {
+        step(t, sa, sb);
+        if (t + 1 < n_tiles) step(t + 1, sb, sa);
     }
 
     l_run += __shfl_xor(l_run, 32);  // the two lane halves hold different keys of the row
