@@ -37,12 +37,19 @@
 // f32 kernel: a plain wave-per-query-row online-softmax kernel; Crane serves
 // prefill in bf16 on GPU (crane-serve/src/lib.rs:123-150), f32 is kept for
 // completeness of the operator.
+#include <type_traits>
+
 #include "common.h"
 
 namespace crane {
 namespace {
 
-constexpr int kBM = 128;                      // query rows per workgroup
+#ifndef CRANE_PREFILL_WAVES
+#define CRANE_PREFILL_WAVES 4
+#endif
+constexpr int kWaves = CRANE_PREFILL_WAVES;   // waves per workgroup, 32 query rows each
+constexpr int kBM = 32 * kWaves;              // query rows per workgroup
+constexpr int kCopies = 16 / kWaves;          // 1 KiB blocks of a 16 KiB tile each wave copies
 constexpr int kBN = 64;                       // keys per tile
 constexpr int kTileBytes = kBN * kHeadDim * 2;  // 16 KiB of K (or V) per tile
 constexpr float kLazy = 8.0f;                 // log2-domain slack before the running max moves
@@ -53,11 +60,13 @@ __device__ __forceinline__ f32x16_v mfma32(bf16x8_v a, bf16x8_v b, f32x16_v c) {
 
 __device__ __forceinline__ bf16x8_v as_bf16x8(uint4 u) { return __builtin_bit_cast(bf16x8_v, u); }
 
-// LDS tiles keep Crane's row-major rows (256 B per key) with the 16-byte chunks
-// of row r XOR-permuted by swz(r): 16 consecutive rows read at one chunk index
-// (K fragments) hit 16 different chunks, and the 4-row x 2-chunk blocks of the
-// transposed V reads hit 8 different chunks.
-__device__ __forceinline__ int swz(int row) { return ((row & 3) << 1) | ((row >> 2) & 1) | (((row >> 3) & 1) << 3); }
+// LDS tiles keep Crane's row-major rows (256 B per key, a full sweep of the 64
+// banks) with the 16-byte chunks of row r XOR-permuted by swz(r), which swaps
+// the two 2-bit halves of r mod 16.  Then 16 consecutive rows read at one chunk
+// index (K fragments, 16 lanes per cycle) hit 16 different chunks, and a
+// transposed V read (32 lanes per cycle: 4 rows x 4 consecutive chunks) hits
+// 16 different chunks, so neither read pattern has bank conflicts.
+__device__ __forceinline__ int swz(int row) { return ((row & 3) << 2) | ((row >> 2) & 3); }
 
 typedef __attribute__((__vector_size__(4 * sizeof(short)))) short s16x4_v;
 typedef __attribute__((address_space(3))) s16x4_v lds_s16x4_v;
@@ -77,16 +86,20 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, in
 
 // Copy keys [64 t, 64 t + 64) of K (or V) into one 16 KiB LDS buffer with
 // bounds-checked buffer_load ... lds (rows past the cache rows read as zero).
-// Wave w copies the 1 KiB blocks 4w..4w+3 of the tile; lane l of block blk
-// fills row 4 blk + l/16, chunk l%16, with global chunk (l%16) ^ swz(row).
-__device__ __forceinline__ void issue_tile(__amdgpu_buffer_rsrc_t rsrc, int t, int wave, int lane, uint8_t* dst) {
+// Wave w copies the 1 KiB blocks kCopies*w .. +kCopies-1 of the tile; lane l of
+// block blk fills row 4 blk + l/16, chunk l%16, with global chunk (l%16) ^ swz(row).
+__device__ __forceinline__ int copy_voffset(int i, int wave, int lane) {
+    const int row = 4 * (wave * kCopies + i) + (lane >> 4);
+    return row * (kHeadDim * 2) + 16 * ((lane & 15) ^ swz(row));
+}
+// vofs[i] = copy_voffset(i, ...): the lane part of the source offset, fixed per
+// lane; the tile part (t * 16 KiB) is the wave-uniform soffset.
+__device__ __forceinline__ void issue_tile(__amdgpu_buffer_rsrc_t rsrc, int t, int wave, const uint32_t (&vofs)[kCopies],
+                                           uint8_t* dst) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int blk = wave * 4 + i;
-        const int row = 4 * blk + (lane >> 4);
-        const int off = (t * kBN + row) * (kHeadDim * 2) + 16 * ((lane & 15) ^ swz(row));
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, dst + blk * 1024, 16, off, 0, 0, 0);
-    }
+    for (int i = 0; i < kCopies; ++i)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, dst + (wave * kCopies + i) * 1024, 16, vofs[i], t * kTileBytes,
+                                                 0, 0);
 }
 
 // s_waitcnt with only vmcnt constrained (expcnt and lgkmcnt at their maxima).
@@ -94,7 +107,9 @@ __device__ __forceinline__ void issue_tile(__amdgpu_buffer_rsrc_t rsrc, int t, i
 
 // S^T = K Q^T for the 64 keys of a tile: two 32x32 blocks of 8 MFMAs each.
 // Lane (n, hh) holds keys nb*32 + 8*(r/4) + 4*hh + r%4 of query row n in s[nb][r].
-__device__ __forceinline__ void qk_tile(const uint8_t* kt_lds, const bf16x8_v (&qf)[8], int n, int hh,
+// koff[ks] is the lane's byte offset of chunk 2ks+hh of row n; row 32+n has the
+// same swizzle (it depends on the row mod 16), so block nb adds nb * 8 KiB.
+__device__ __forceinline__ void qk_tile(const uint8_t* kt_lds, const bf16x8_v (&qf)[8], const uint32_t (&koff)[8],
                                         f32x16_v (&s)[2]) {
 #pragma unroll
     for (int nb = 0; nb < 2; ++nb)
@@ -104,10 +119,16 @@ __device__ __forceinline__ void qk_tile(const uint8_t* kt_lds, const bf16x8_v (&
     for (int ks = 0; ks < 8; ++ks)
 #pragma unroll
         for (int nb = 0; nb < 2; ++nb) {
-            const int row = nb * 32 + n;
-            const uint4 ku = *reinterpret_cast<const uint4*>(kt_lds + row * 256 + 16 * ((2 * ks + hh) ^ swz(row)));
+            const uint4 ku = *reinterpret_cast<const uint4*>(kt_lds + koff[ks] + nb * 8192);
             s[nb] = mfma32(as_bf16x8(ku), qf[ks], s[nb]);
         }
+}
+
+// Keep a value in a register as computed: the compiler may not split it into
+// a base plus a per-use offset (which would cost an add per use in the loop).
+__device__ __forceinline__ uint32_t pinned(uint32_t v) {
+    asm volatile("" : "+v"(v));
+    return v;
 }
 
 // Map the 1-D workgroup id to (q tile, sequence, q head).  Groups of
@@ -131,7 +152,7 @@ __device__ __forceinline__ bool map_block(int id, int n_qt, int B, int Hkv, int 
 }
 
 template <bool CAUSAL>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void prefill_bf16_kernel(
+__global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(2, 2))) void prefill_bf16_kernel(
     const bf16_t* __restrict__ q, const bf16_t* __restrict__ kc, const bf16_t* __restrict__ vc, int64_t cap,
     const int32_t* __restrict__ start_pos, int max_start, int S, int B, int Hq, int Hkv, float scale_log2,
     bf16_t* __restrict__ out) {
@@ -149,7 +170,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     __shared__ __attribute__((aligned(1024))) uint8_t vbuf[2][kTileBytes];
 
     const int tid = threadIdx.x;
-    const int lane = tid & 63, wave = tid >> 6;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: LDS copy targets are scalar
     const int n = lane & 31, hh = lane >> 5;
 
     const int L = start + S;                                 // cache rows holding keys for this chunk
@@ -158,9 +180,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     const int64_t head0 = ((int64_t)b * Hkv + kvh) * cap * kHeadDim;
     const __amdgpu_buffer_rsrc_t rk = make_rsrc(kc + head0, L * kHeadDim * 2);
     const __amdgpu_buffer_rsrc_t rv = make_rsrc(vc + head0, L * kHeadDim * 2);
-    issue_tile(rk, 0, wave, lane, kbuf[0]);
-    issue_tile(rv, 0, wave, lane, vbuf[0]);
-    if (n_tiles > 1) issue_tile(rk, 1, wave, lane, kbuf[1]);
+    uint32_t vofs[kCopies];
+#pragma unroll
+    for (int i = 0; i < kCopies; ++i) vofs[i] = pinned(copy_voffset(i, wave, lane));
+    issue_tile(rk, 0, wave, vofs, kbuf[0]);
+    issue_tile(rv, 0, wave, vofs, vbuf[0]);
+    if (n_tiles > 1) issue_tile(rk, 1, wave, vofs, kbuf[1]);
 
     // Q fragments (B operand of S^T = K Q^T): query row qrow, dims 16ks + 8hh .. +7.
     const int qrow = m0 + wave * 32 + n;
@@ -187,21 +212,38 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     const int v_h = vg >> 1;                            // key half of the A operand
     const int v_col = 16 * (vg & 1) + 4 * (vi & 3);     // column inside a 32-dim block
     const bf16x2_v ones = {(__bf16)1.f, (__bf16)1.f};
+    // Per-lane LDS byte offsets, fixed for the whole loop.  K: chunk 2ks+hh of
+    // row n.  V (transposed reads): rows r = 4 v_h + vi/4 (+8 for the high
+    // half) at column 32 db + v_col; key step st adds 16 rows = 4 KiB, with
+    // the same swizzle (rows mod 16 are unchanged).
+    uint32_t koff[8], voff[4][2];
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) koff[ks] = pinned(n * 256 + 16 * ((2 * ks + hh) ^ swz(n)));
+#pragma unroll
+    for (int db = 0; db < 4; ++db)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int r = 4 * v_h + (vi >> 2) + 8 * h, col = 32 * db + v_col;
+            voff[db][h] = pinned(r * 256 + 16 * ((col >> 3) ^ swz(r)) + 2 * (col & 7));
+        }
 
     // Tile 0 is visible to every row (key 0 precedes every query position).
-    if (n_tiles > 1) CRANE_WAIT_VMCNT(8); else CRANE_WAIT_VMCNT(4);  // this wave's K(0) copies
+    if (n_tiles > 1) CRANE_WAIT_VMCNT(2 * kCopies); else CRANE_WAIT_VMCNT(kCopies);  // this wave's K(0) copies
     __syncthreads();                                                   // ... and every wave's
     f32x16_v sa[2], sb[2];
-    qk_tile(kbuf[0], qf, n, hh, sa);
+    qk_tile(kbuf[0], qf, koff, sa);
 
     // One tile: softmax of tile t's scores (sc), S^T of tile t+1 (into sn),
     // then O^T += V^T P^T for tile t.  The exp work of tile t and the MFMAs of
     // tile t+1 are independent, so one wave keeps both pipes busy.
-    auto step = [&](int t, f32x16_v (&sc)[2], f32x16_v (&sn)[2]) {
+    // The step's parity (t & 1) is a compile-time constant, so every LDS
+    // address below is a per-lane offset plus an immediate.
+    auto step = [&](auto parity, int t, f32x16_v (&sc)[2], f32x16_v (&sn)[2]) {
+        constexpr int par = decltype(parity)::value;
         CRANE_WAIT_VMCNT(0);  // this wave's copies of V(t) and K(t+1) have landed
         __syncthreads();      // ... and every wave's; K(t) and V(t-1) are fully consumed
-        if (t + 2 < n_tiles) issue_tile(rk, t + 2, wave, lane, kbuf[t & 1]);
-        if (t + 1 < n_tiles) issue_tile(rv, t + 1, wave, lane, vbuf[(t + 1) & 1]);
+        if (t + 2 < n_tiles) issue_tile(rk, t + 2, wave, vofs, kbuf[par]);
+        if (t + 1 < n_tiles) issue_tile(rv, t + 1, wave, vofs, vbuf[par ^ 1]);
         const int kt = t * kBN;
         if (CAUSAL && kt > wave_first + 31) return;  // the whole tile is above this wave's diagonal
         if (kt + kBN > kend || (CAUSAL && kt + kBN - 1 > wave_first)) {  // diagonal or last tile
@@ -262,27 +304,24 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         // Unconditional, so this stays in one basic block with the exp work
         // above: past the last tile (or above this wave's diagonal) the
         // result is simply not used, and nothing is in flight into that buffer.
-        qk_tile(kbuf[(t + 1) & 1], qf, n, hh, sn);
+        qk_tile(kbuf[par ^ 1], qf, koff, sn);
         // ---- O^T += V^T P^T: 4 dim blocks x 4 key steps of 16; the A operand
         // (dims x keys) comes straight from the row-major V tile by transposed reads
-        const uint8_t* vt_lds = vbuf[t & 1];
+        const uint8_t* vt_lds = vbuf[par];
 #pragma unroll
         for (int st = 0; st < 4; ++st) {
-            const int r0 = 16 * st + 4 * v_h + (vi >> 2);  // keys of slots 0..3; slots 4..7 are 8 rows on
-            const int r1 = r0 + 8;
 #pragma unroll
             for (int db = 0; db < 4; ++db) {
-                const int col = 32 * db + v_col;
-                const uint2 lo = read_tr16(vt_lds + r0 * 256 + 16 * ((col >> 3) ^ swz(r0)) + 2 * (col & 7));
-                const uint2 hi = read_tr16(vt_lds + r1 * 256 + 16 * ((col >> 3) ^ swz(r1)) + 2 * (col & 7));
+                const uint2 lo = read_tr16(vt_lds + voff[db][0] + st * 4096);  // keys of slots 0..3
+                const uint2 hi = read_tr16(vt_lds + voff[db][1] + st * 4096);  // slots 4..7: 8 rows on
                 const uint4 vu = make_uint4(lo.x, lo.y, hi.x, hi.y);
                 oacc[db] = mfma32(as_bf16x8(vu), pf[st], oacc[db]);
             }
         }
     };
     for (int t = 0; t < n_tiles; t += 2) {
-        step(t, sa, sb);
-        if (t + 1 < n_tiles) step(t + 1, sb, sa);
+        step(std::integral_constant<int, 0>{}, t, sa, sb);
+        if (t + 1 < n_tiles) step(std::integral_constant<int, 1>{}, t + 1, sb, sa);
     }
 
     l_run += __shfl_xor(l_run, 32);  // the two lane halves hold different keys of the row
@@ -364,11 +403,11 @@ extern "C" int crane_hip_attn_prefill(const void* q, const void* k_cache, const 
         const int64_t blocks = ((units + 7) / 8) * chunk;
         if (blocks > 0x7fffffffLL) return CRANE_HIP_E_INVALID;
         if (causal)
-            hipLaunchKernelGGL(prefill_bf16_kernel<true>, dim3((unsigned)blocks), dim3(256), 0, st,
+            hipLaunchKernelGGL(prefill_bf16_kernel<true>, dim3((unsigned)blocks), dim3(64 * kWaves), 0, st,
                                (const bf16_t*)q, (const bf16_t*)k_cache, (const bf16_t*)v_cache, cache_cap, start_pos,
                                (int)max_start, S, B, Hq, Hkv, sl, (bf16_t*)out);
         else
-            hipLaunchKernelGGL(prefill_bf16_kernel<false>, dim3((unsigned)blocks), dim3(256), 0, st,
+            hipLaunchKernelGGL(prefill_bf16_kernel<false>, dim3((unsigned)blocks), dim3(64 * kWaves), 0, st,
                                (const bf16_t*)q, (const bf16_t*)k_cache, (const bf16_t*)v_cache, cache_cap, start_pos,
                                (int)max_start, S, B, Hq, Hkv, sl, (bf16_t*)out);
     } else {
