@@ -1,4 +1,5 @@
-"""ctypes binding of libcrane_hip.so, the C ABI declared in include/crane_hip.h.
+"""ctypes binding of libcrane_hip.so, the C ABI declared in include/crane_hip.h
+(attention launchers) and include/crane_kv.h (host-side KV-cache manager).
 
 The library is the only compute path: there is no CPU fallback.  Loading
 fails loudly when the built library is missing.
@@ -17,9 +18,10 @@ NORM_THEN_ROPE, ROPE_THEN_NORM, ROPE_ONLY = 0, 1, 2
 OK = 0
 E_INVALID, E_DTYPE, E_HEAD_DIM, E_GQA, E_CAPACITY, E_WORKSPACE, E_LAUNCH, E_ALIGN = range(1, 9)
 
-# Every symbol include/crane_hip.h declares, with its ctypes signature.
+# Every symbol include/*.h declares, with its ctypes signature.
 _vp, _i32p, _i64, _i, _f, _sz = (ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64, ctypes.c_int,
                                  ctypes.c_float, ctypes.c_size_t)
+_vpp, _i64p, _u64 = ctypes.POINTER(ctypes.c_void_p), ctypes.POINTER(ctypes.c_int64), ctypes.c_uint64
 SIGNATURES = {
     "crane_hip_strerror": ([_i], ctypes.c_char_p),
     "crane_hip_version": ([], ctypes.c_char_p),
@@ -31,6 +33,21 @@ SIGNATURES = {
         [_vp, _vp, _vp, _i64, _i32p, _i64, _i, _i, _i, _i, _f, _vp, _sz, _vp, _i, _vp], _i),
     "crane_hip_attn_prefill": (
         [_vp, _vp, _vp, _i64, _i32p, _i64, _i, _i, _i, _i, _i, _f, _i, _vp, _i, _vp], _i),
+    # include/crane_kv.h
+    "crane_kv_grown_capacity": ([_i64, _i64], _i64),
+    "crane_kv_create": ([_i, _i, _i, _i, _vpp], _i),
+    "crane_kv_destroy": ([_vp], None),
+    "crane_kv_reserve": ([_vp, _i64, _vp], _i),
+    "crane_kv_update": ([_vp, _vp, _vp, _i, _vp], _i),
+    "crane_kv_append_qkv": (
+        [_vp, _vp, _i64, _vp, _vp, _f, _i, _vp, _vp, _i64, _i64, _i32p, _vp, _i, _i, _vp], _i),
+    "crane_kv_decode": ([_vp, _vp, _i, _f, _vp, _sz, _vp, _vp], _i),
+    "crane_kv_prefill": ([_vp, _vp, _i, _i, _f, _i, _vp, _vp], _i),
+    "crane_kv_views": ([_vp, _vpp, _vpp, _i64p, _vpp, _i64p], _i),
+    "crane_kv_set_lengths": ([_vp, _i64p, _vp], _i),
+    "crane_kv_bytes": ([_vp], _u64),
+    "crane_kv_stack": ([_vp, _vpp, _i, _i64, _vp], _i),
+    "crane_kv_extract": ([_vp, _i, _vp, _vp], _i),
 }
 
 

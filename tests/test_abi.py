@@ -11,23 +11,29 @@ import pytest
 from crane_amd import _lib
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-HEADER = os.path.join(ROOT, "include", "crane_hip.h")
+HEADERS = [os.path.join(ROOT, "include", h) for h in sorted(os.listdir(os.path.join(ROOT, "include")))
+           if h.endswith(".h")]
 
 
 def _declared():
-    text = open(HEADER).read()
-    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
     decls = {}
-    for m in re.finditer(r"\b(?:int|size_t|const char\s*\*)\s+(crane_hip_\w+)\s*\(([^)]*)\)\s*;", text):
-        args = [a for a in m.group(2).split(",") if a.strip() and a.strip() != "void"]
-        decls[m.group(1)] = len(args)
+    for header in HEADERS:
+        text = re.sub(r"/\*.*?\*/", "", open(header).read(), flags=re.S)
+        for m in re.finditer(r"\b(?:int|void|size_t|int64_t|uint64_t|const char\s*\*)\s+(crane_\w+)\s*"
+                             r"\(([^)]*)\)\s*;", text):
+            args = [a for a in m.group(2).split(",") if a.strip() and a.strip() != "void"]
+            decls[m.group(1)] = len(args)
     return decls
 
 
 def test_header_declares_the_path():
     d = _declared()
-    assert set(d) == {"crane_hip_strerror", "crane_hip_version", "crane_hip_qknorm_rope_append",
-                      "crane_hip_attn_decode_workspace", "crane_hip_attn_decode", "crane_hip_attn_prefill"}
+    assert {"crane_hip_strerror", "crane_hip_version", "crane_hip_qknorm_rope_append",
+            "crane_hip_attn_decode_workspace", "crane_hip_attn_decode", "crane_hip_attn_prefill"} <= set(d)
+    assert {"crane_kv_grown_capacity", "crane_kv_create", "crane_kv_destroy", "crane_kv_reserve",
+            "crane_kv_update", "crane_kv_append_qkv", "crane_kv_decode", "crane_kv_prefill", "crane_kv_views",
+            "crane_kv_set_lengths", "crane_kv_bytes", "crane_kv_stack", "crane_kv_extract"} <= set(d)
+    assert set(d) == set(_lib.SIGNATURES), set(d) ^ set(_lib.SIGNATURES)
 
 
 def test_library_exports_every_declared_symbol():
