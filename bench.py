@@ -200,6 +200,54 @@ def bench_decode_c5(args, dev, stream, lib):
     return dict(ms=ms, gbs=gbs, algo_bytes=algo)
 
 
+def bench_decode_paged(args, dev, stream, lib):
+    """Config 3 over the paged layout: the same lengths, K/V in pools of
+    256-row pages whose ids are shuffled over the pool, read in place through
+    the block table (crane_hip_attn_decode_paged)."""
+    import torch
+    lens = c3_lengths()
+    B, Hq, Hkv, P = 32, 32, 8, 256
+    kv_len = lens + 1
+    need = [(int(n) + P - 1) // P for n in kv_len]
+    stride, n_pages = max(need), sum(need)
+    R = 3
+    gen = torch.Generator(device=dev).manual_seed(SEED0 + 3)
+    pools = [(randn((n_pages, Hkv, P, D), gen, torch.bfloat16, dev), randn((n_pages, Hkv, P, D), gen, torch.bfloat16,
+                                                                          dev)) for _ in range(R)]
+    perm = np.random.Generator(np.random.PCG64(SEED0 + 3)).permutation(n_pages).astype(np.int32)
+    table = np.full((B, stride), -1, np.int32)
+    nxt = 0
+    for b in range(B):
+        table[b, :need[b]] = perm[nxt:nxt + need[b]]
+        nxt += need[b]
+    table_d = torch.as_tensor(table, device=dev)
+    q = randn((B, Hq, D), gen, torch.bfloat16, dev)
+    out = torch.empty((B, 1, Hq * D), dtype=torch.bfloat16, device=dev)
+    kv_len_d = torch.as_tensor(kv_len, device=dev)
+    mx = int(kv_len.max())
+    ws_need = lib.crane_hip_attn_decode_workspace(B, Hq, Hkv, D, mx, 1)
+    ws = torch.zeros(ws_need, dtype=torch.uint8, device=dev)
+    st = stream.cuda_stream
+    fn = lib.crane_hip_attn_decode_paged
+
+    def launch(i):
+        kp, vp = pools[i % R]
+        rc = fn(q.data_ptr(), kp.data_ptr(), vp.data_ptr(), n_pages, P, table_d.data_ptr(), stride,
+                kv_len_d.data_ptr(), mx, B, Hq, Hkv, D, 1.0 / math.sqrt(D), ws.data_ptr(), ws_need, out.data_ptr(), 1,
+                st)
+        if rc:
+            raise RuntimeError(f"crane_hip_attn_decode_paged failed: {rc}")
+
+    ms = timed(launch, args.steps, args.warmup, stream)
+    algo = int(kv_len.sum()) * Hkv * D * 2 * 2 + 2 * B * Hq * D * 2
+    gbs = algo / (ms * 1e-3) / 1e9
+    log(f"[decode c3 paged] {ms * 1e3:.2f} us/step, {gbs:.1f} GB/s ({gbs / HBM_PEAK_GBS * 100:.1f}% of HBM), "
+        f"{n_pages} pages of {P} rows")
+    del pools
+    torch.cuda.empty_cache()
+    return dict(ms=ms, gbs=gbs, page_rows=P, n_pages=n_pages)
+
+
 # ---------------------------------------------------------------- prefill
 
 def bench_prefill(args, dev, stream, lib):
@@ -416,11 +464,12 @@ def main():
         log("[calibration] 3 x neg over 2^28 f32 (1073741824 B read + 1073741824 B written each)")
         del src, dst
         torch.cuda.empty_cache()
-    dec = pre = c5 = c2 = app = None
+    dec = pre = c5 = c2 = app = pg = None
     if args.only in ("decode", "all"):
         dec = bench_decode(args, dev, stream, lib)
         if args.only == "all":
             c5 = bench_decode_c5(args, dev, stream, lib)
+            pg = bench_decode_paged(args, dev, stream, lib)
     if args.only in ("prefill", "all"):
         pre = bench_prefill(args, dev, stream, lib)
         if args.only == "all":
@@ -468,6 +517,11 @@ def main():
         line["decode_c5"] = {"workload": "c5: Qwen2.5-72B-shape decode, B=8, 64/8 heads, L=32768+1",
                              "value": round(c5["gbs"], 2), "unit": "GB/s", "us_per_step": round(c5["ms"] * 1e3, 2),
                              "frac": round(c5["gbs"] / HBM_PEAK_GBS, 4)}
+    if pg is not None:
+        line["decode_c3_paged"] = {"workload": "c3 over a paged cache (shuffled 256-row pages, block table)",
+                                   "value": round(pg["gbs"], 2), "unit": "GB/s",
+                                   "us_per_step": round(pg["ms"] * 1e3, 2), "frac": round(pg["gbs"] / HBM_PEAK_GBS, 4),
+                                   "kernel": "decode_chunk_kernel<PagedRows> + decode_merge_kernel"}
     if c2 is not None:
         line["prefill_c2"] = {"workload": "c2: Qwen3-0.6B-shape append+causal prefill, S=2048, 16/8 heads",
                               "us_per_step": round(c2["ms"] * 1e3, 2), "tflops": round(c2["tflops"], 2)}

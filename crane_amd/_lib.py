@@ -1,5 +1,6 @@
 """ctypes binding of libcrane_hip.so, the C ABI declared in include/crane_hip.h
-(attention launchers) and include/crane_kv.h (host-side KV-cache manager).
+(attention launchers, dense and paged), include/crane_kv.h (host-side KV-cache
+manager) and include/crane_pkv.h (paged KV-cache manager).
 
 The library is the only compute path: there is no CPU fallback.  Loading
 fails loudly when the built library is missing.
@@ -22,6 +23,7 @@ E_INVALID, E_DTYPE, E_HEAD_DIM, E_GQA, E_CAPACITY, E_WORKSPACE, E_LAUNCH, E_ALIG
 _vp, _i32p, _i64, _i, _f, _sz = (ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64, ctypes.c_int,
                                  ctypes.c_float, ctypes.c_size_t)
 _vpp, _i64p, _u64 = ctypes.POINTER(ctypes.c_void_p), ctypes.POINTER(ctypes.c_int64), ctypes.c_uint64
+_ip = ctypes.POINTER(ctypes.c_int)
 SIGNATURES = {
     "crane_hip_strerror": ([_i], ctypes.c_char_p),
     "crane_hip_version": ([], ctypes.c_char_p),
@@ -48,6 +50,31 @@ SIGNATURES = {
     "crane_kv_bytes": ([_vp], _u64),
     "crane_kv_stack": ([_vp, _vpp, _i, _i64, _vp], _i),
     "crane_kv_extract": ([_vp, _i, _vp, _vp], _i),
+    # include/crane_hip.h, paged layout
+    "crane_hip_qknorm_rope_append_paged": (
+        [_vp, _i64, _vp, _vp, _f, _i, _vp, _vp, _i64, _i64, _i32p, _vp, _vp, _vp, _i64, _i, _i32p, _i64, _i32p,
+         _i, _i, _i, _i, _i, _i, _vp], _i),
+    "crane_hip_attn_decode_paged": (
+        [_vp, _vp, _vp, _i64, _i, _i32p, _i64, _i32p, _i64, _i, _i, _i, _i, _f, _vp, _sz, _vp, _i, _vp], _i),
+    "crane_hip_attn_prefill_paged": (
+        [_vp, _vp, _vp, _i64, _i, _i32p, _i64, _i32p, _i64, _i, _i, _i, _i, _i, _f, _i, _vp, _i, _vp], _i),
+    # include/crane_pkv.h
+    "crane_pkv_create": ([_i, _i, _i, _i, _i64, _i, _i, _vpp], _i),
+    "crane_pkv_destroy": ([_vp], None),
+    "crane_pkv_seq_add": ([_vp, _ip], _i),
+    "crane_pkv_seq_free": ([_vp, _i], _i),
+    "crane_pkv_seq_len": ([_vp, _i], _i64),
+    "crane_pkv_free_pages": ([_vp], _i64),
+    "crane_pkv_bytes": ([_vp], _u64),
+    "crane_pkv_set_batch": ([_vp, _ip, _i, _vp], _i),
+    "crane_pkv_update": ([_vp, _vp, _vp, _i, _vp], _i),
+    "crane_pkv_append_qkv": (
+        [_vp, _vp, _i64, _vp, _vp, _f, _i, _vp, _vp, _i64, _i64, _i32p, _vp, _i, _i, _vp], _i),
+    "crane_pkv_decode": ([_vp, _vp, _i, _f, _vp, _sz, _vp, _vp], _i),
+    "crane_pkv_prefill": ([_vp, _vp, _i, _i, _f, _i, _vp, _vp], _i),
+    "crane_pkv_read_seq": ([_vp, _i, _vp, _vp, _vp], _i),
+    "crane_pkv_write_seq": ([_vp, _i, _vp, _vp, _i64, _vp], _i),
+    "crane_pkv_views": ([_vp, _vpp, _vpp, _vpp, _i64p, _vpp], _i),
 }
 
 

@@ -69,12 +69,12 @@ __device__ __forceinline__ void rope4(float (&x1)[4], float (&x2)[4], const floa
     }
 }
 
-template <typename T>
+template <typename T, class ROWS>
 __global__ __launch_bounds__(256) void qknorm_rope_append_kernel(
     const T* __restrict__ qkv, int64_t row_stride, const T* __restrict__ qw, const T* __restrict__ kw,
     float eps, int order, const T* __restrict__ cos_t, const T* __restrict__ sin_t, int64_t cs_stride,
     int64_t table_rows, const int32_t* __restrict__ positions, T* __restrict__ q_out, T* __restrict__ k_cache,
-    T* __restrict__ v_cache, int64_t cap, const int32_t* __restrict__ cache_len, int S, int Hq, int Hkv,
+    T* __restrict__ v_cache, ROWS rows, const int32_t* __restrict__ cache_len, int S, int Hq, int Hkv,
     int64_t n_items) {
     const int64_t item = (int64_t)blockIdx.x * kItemsPerBlock + (threadIdx.x >> 4);
     const int l = threadIdx.x & 15;
@@ -91,9 +91,9 @@ __global__ __launch_bounds__(256) void qknorm_rope_append_kernel(
     load4(src + 64 + 4 * l, x2);
 
     if (head >= Hq + Hkv) {  // value row: straight into the cache
-        const int64_t row = (int64_t)cache_len[b] + s;
-        if (row < 0 || row >= cap) return;
-        T* dst = v_cache + (((int64_t)b * Hkv + (head - Hq - Hkv)) * cap + row) * kHeadDim;
+        const int64_t off = rows.offset(b, Hkv, head - Hq - Hkv, (int64_t)cache_len[b] + s);
+        if (off < 0) return;  // past the capacity (or on an invalid page): not written
+        T* dst = v_cache + off;
         store4(dst + 4 * l, x1);
         store4(dst + 64 + 4 * l, x2);
         return;
@@ -103,9 +103,9 @@ __global__ __launch_bounds__(256) void qknorm_rope_append_kernel(
     if (is_q) {
         dst = q_out + (((int64_t)b * Hq + head) * S + s) * kHeadDim;
     } else {
-        const int64_t row = (int64_t)cache_len[b] + s;
-        if (row < 0 || row >= cap) return;
-        dst = k_cache + (((int64_t)b * Hkv + (head - Hq)) * cap + row) * kHeadDim;
+        const int64_t off = rows.offset(b, Hkv, head - Hq, (int64_t)cache_len[b] + s);
+        if (off < 0) return;
+        dst = k_cache + off;
     }
     const T* w = is_q ? qw : kw;
     const int64_t p = (int64_t)positions[b] + s;
@@ -124,26 +124,18 @@ __global__ __launch_bounds__(256) void qknorm_rope_append_kernel(
     store4(dst + 64 + 4 * l, x2);
 }
 
-}  // namespace
-}  // namespace crane
-
-using namespace crane;
-
-extern "C" int crane_hip_qknorm_rope_append(const void* qkv, int64_t qkv_row_stride, const void* q_norm_w,
-                                            const void* k_norm_w, float eps, int order, const void* cos,
-                                            const void* sin, int64_t cs_stride, int64_t table_rows,
-                                            const int32_t* positions,
-                                            void* q_out, void* k_cache, void* v_cache, int64_t cache_cap,
-                                            const int32_t* cache_len, int64_t max_rows, int B, int S, int Hq,
-                                            int Hkv, int D, int dtype, void* stream) {
+// Checks shared by both layouts, then the launch; `rows` addresses the cache.
+template <class ROWS>
+int qknorm_rope_append(const void* qkv, int64_t qkv_row_stride, const void* q_norm_w, const void* k_norm_w,
+                       float eps, int order, const void* cos, const void* sin, int64_t cs_stride, int64_t table_rows,
+                       const int32_t* positions, void* q_out, void* k_cache, void* v_cache, const ROWS& rows,
+                       const int32_t* cache_len, int B, int S, int Hq, int Hkv, int D, int dtype, void* stream) {
     if (dtype != CRANE_HIP_F32 && dtype != CRANE_HIP_BF16) return CRANE_HIP_E_DTYPE;
     if (D != kHeadDim) return CRANE_HIP_E_HEAD_DIM;
     if (B < 0 || S < 0 || Hq <= 0 || Hkv <= 0) return CRANE_HIP_E_INVALID;
     if (Hq % Hkv != 0) return CRANE_HIP_E_GQA;
     if (order < CRANE_HIP_NORM_THEN_ROPE || order > CRANE_HIP_ROPE_ONLY) return CRANE_HIP_E_INVALID;
     if (!(eps >= 0.0f)) return CRANE_HIP_E_INVALID;
-    if (cache_cap <= 0 || max_rows < 0 || max_rows > cache_cap) return CRANE_HIP_E_CAPACITY;
-    if ((int64_t)S > max_rows) return CRANE_HIP_E_CAPACITY;
     if (B == 0 || S == 0) return CRANE_HIP_OK;
     if (!qkv || !cos || !sin || !positions || !q_out || !k_cache || !v_cache || !cache_len)
         return CRANE_HIP_E_INVALID;
@@ -159,16 +151,53 @@ extern "C" int crane_hip_qknorm_rope_append(const void* qkv, int64_t qkv_row_str
     if (blocks > 0x7fffffffLL) return CRANE_HIP_E_INVALID;
     hipStream_t st = (hipStream_t)stream;
     if (dtype == CRANE_HIP_F32) {
-        hipLaunchKernelGGL(qknorm_rope_append_kernel<float>, dim3((unsigned)blocks), dim3(256), 0, st,
+        hipLaunchKernelGGL((qknorm_rope_append_kernel<float, ROWS>), dim3((unsigned)blocks), dim3(256), 0, st,
                            (const float*)qkv, qkv_row_stride, (const float*)q_norm_w, (const float*)k_norm_w, eps,
                            order, (const float*)cos, (const float*)sin, cs_stride, table_rows, positions, (float*)q_out,
-                           (float*)k_cache, (float*)v_cache, cache_cap, cache_len, S, Hq, Hkv, n_items);
+                           (float*)k_cache, (float*)v_cache, rows, cache_len, S, Hq, Hkv, n_items);
     } else {
-        hipLaunchKernelGGL(qknorm_rope_append_kernel<bf16_t>, dim3((unsigned)blocks), dim3(256), 0, st,
+        hipLaunchKernelGGL((qknorm_rope_append_kernel<bf16_t, ROWS>), dim3((unsigned)blocks), dim3(256), 0, st,
                            (const bf16_t*)qkv, qkv_row_stride, (const bf16_t*)q_norm_w, (const bf16_t*)k_norm_w,
                            eps, order, (const bf16_t*)cos, (const bf16_t*)sin, cs_stride, table_rows, positions,
-                           (bf16_t*)q_out, (bf16_t*)k_cache, (bf16_t*)v_cache, cache_cap, cache_len, S, Hq, Hkv,
+                           (bf16_t*)q_out, (bf16_t*)k_cache, (bf16_t*)v_cache, rows, cache_len, S, Hq, Hkv,
                            n_items);
     }
     return launch_status(hipGetLastError());
+}
+
+}  // namespace
+}  // namespace crane
+
+using namespace crane;
+
+extern "C" int crane_hip_qknorm_rope_append(const void* qkv, int64_t qkv_row_stride, const void* q_norm_w,
+                                            const void* k_norm_w, float eps, int order, const void* cos,
+                                            const void* sin, int64_t cs_stride, int64_t table_rows,
+                                            const int32_t* positions,
+                                            void* q_out, void* k_cache, void* v_cache, int64_t cache_cap,
+                                            const int32_t* cache_len, int64_t max_rows, int B, int S, int Hq,
+                                            int Hkv, int D, int dtype, void* stream) {
+    if (dtype != CRANE_HIP_F32 && dtype != CRANE_HIP_BF16) return CRANE_HIP_E_DTYPE;
+    if (D != kHeadDim) return CRANE_HIP_E_HEAD_DIM;
+    if (cache_cap <= 0 || max_rows < 0 || max_rows > cache_cap) return CRANE_HIP_E_CAPACITY;
+    if ((int64_t)S > max_rows) return CRANE_HIP_E_CAPACITY;
+    return qknorm_rope_append(qkv, qkv_row_stride, q_norm_w, k_norm_w, eps, order, cos, sin, cs_stride, table_rows,
+                              positions, q_out, k_cache, v_cache, DenseRows{cache_cap}, cache_len, B, S, Hq, Hkv, D,
+                              dtype, stream);
+}
+
+extern "C" int crane_hip_qknorm_rope_append_paged(const void* qkv, int64_t qkv_row_stride, const void* q_norm_w,
+                                                  const void* k_norm_w, float eps, int order, const void* cos,
+                                                  const void* sin, int64_t cs_stride, int64_t table_rows,
+                                                  const int32_t* positions, void* q_out, void* k_pool, void* v_pool,
+                                                  int64_t n_pages, int page_rows, const int32_t* block_table,
+                                                  int64_t table_stride, const int32_t* cache_len, int B, int S, int Hq,
+                                                  int Hkv, int D, int dtype, void* stream) {
+    const int rc = check_paged(n_pages, page_rows, block_table, table_stride, Hkv);
+    if (rc) return rc;
+    if ((int64_t)S > table_stride * page_rows) return CRANE_HIP_E_CAPACITY;
+    return qknorm_rope_append(qkv, qkv_row_stride, q_norm_w, k_norm_w, eps, order, cos, sin, cs_stride, table_rows,
+                              positions, q_out, k_pool, v_pool,
+                              PagedRows{block_table, table_stride, n_pages, page_rows}, cache_len, B, S, Hq, Hkv, D,
+                              dtype, stream);
 }

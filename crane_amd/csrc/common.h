@@ -84,6 +84,39 @@ __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_ex
 
 constexpr float kLog2e = 1.4426950408889634f;
 
+// Where row j of (sequence b, kv head kvh) of the K or V cache lives.
+// offset() is the element offset of the row inside its buffer, or -1 when the
+// row is past the sequence's capacity or its page id is outside the pool
+// (such a row is never read or written).
+//
+// Dense: Crane's contiguous [B, Hkv, cap, D] buffers.
+struct DenseRows {
+    static constexpr bool kPaged = false;
+    int64_t cap;
+    __device__ __forceinline__ int64_t offset(int b, int Hkv, int kvh, int64_t j) const {
+        if (j < 0 || j >= cap) return -1;
+        return (((int64_t)b * Hkv + kvh) * cap + j) * kHeadDim;
+    }
+};
+// Paged: pools [n_pages, Hkv, page_rows, D]; row j of sequence b is row
+// j % page_rows of page table[b * stride + j / page_rows].
+struct PagedRows {
+    static constexpr bool kPaged = true;
+    const int32_t* table;
+    int64_t stride;
+    int64_t n_pages;
+    int page_rows;
+    __device__ __forceinline__ int64_t offset(int b, int Hkv, int kvh, int64_t j) const {
+        if (j < 0 || j >= stride * page_rows) return -1;
+        // The table is read-only for the kernel's lifetime: read it through
+        // the constant address space, so a wave-uniform lookup is a scalar load.
+        typedef const __attribute__((address_space(4))) int32_t* table_t;
+        const int64_t page = ((table_t)table)[b * stride + j / page_rows];
+        if (page < 0 || page >= n_pages) return -1;
+        return ((page * Hkv + kvh) * page_rows + j % page_rows) * kHeadDim;
+    }
+};
+
 }  // namespace crane
 
 // Host-side helpers shared by the launchers.
@@ -97,5 +130,14 @@ inline float bits_f32(uint32_t u) { return __builtin_bit_cast(float, u); }
 inline float host_round_bf16(float f) {
     const uint32_t u = f32_bits(f);
     return bits_f32((u + 0x7fffu + ((u >> 16) & 1u)) & 0xffff0000u);
+}
+// Host checks of a paged cache description: pools [n_pages, Hkv, page_rows, D]
+// and a block table of `stride` page ids per sequence.
+inline int check_paged(int64_t n_pages, int page_rows, const int32_t* table, int64_t stride, int Hkv) {
+    if (n_pages <= 0 || page_rows <= 0 || page_rows % CRANE_HIP_PAGE_ALIGN != 0 || stride <= 0 || !table)
+        return CRANE_HIP_E_INVALID;
+    if (n_pages > 0x7fffffffLL || stride > 0x7fffffffLL / page_rows) return CRANE_HIP_E_INVALID;
+    if (Hkv > 0 && n_pages > ((int64_t)1 << 62) / ((int64_t)Hkv * page_rows * kHeadDim)) return CRANE_HIP_E_INVALID;
+    return CRANE_HIP_OK;
 }
 }  // namespace crane

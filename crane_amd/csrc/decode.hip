@@ -142,10 +142,10 @@ struct DecodeShared {
 // One work item: chunk c (keys [c kChunk, (c+1) kChunk)) of sequence b for the
 // G q heads of head group gi.  Writes the normalised rows when the sequence
 // fits one chunk, otherwise the unnormalised partial and its (max, sum).
-template <typename T, int G>
+template <typename T, int G, class ROWS>
 __device__ __forceinline__ void decode_item(
     DecodeShared<T, G>& sm, const T* __restrict__ q, const T* __restrict__ kc, const T* __restrict__ vc,
-    int64_t cap, int L, int b, int gi, int c, int Hq, int Hkv, int n_rep, float scale, int nsplit,
+    const ROWS& rows, int L, int b, int gi, int c, int Hq, int Hkv, int n_rep, float scale, int nsplit,
     float* __restrict__ ws_o, float* __restrict__ ws_ml, T* __restrict__ out) {
     constexpr bool kBf16 = std::is_same<T, bf16_t>::value;
     constexpr int kVecA = 16 * (int)sizeof(T) / 16;  // 16-byte loads per lane per K row (16 dims)
@@ -189,10 +189,13 @@ __device__ __forceinline__ void decode_item(
             for (int i = 0; i < 16; ++i) qf[h][i] = x[i] * scale_t;
         }
     }
-    // Rows [j0, j0 + n) of this (sequence, kv head); loads past them return 0.
-    const int64_t row0 = ((int64_t)b * Hkv + kvh) * cap + j0;
-    const __amdgpu_buffer_rsrc_t rk = make_rsrc(kc + row0 * kHeadDim, n * kHeadDim * (int)sizeof(T));
-    const __amdgpu_buffer_rsrc_t rv = make_rsrc(vc + row0 * kHeadDim, n * kHeadDim * (int)sizeof(T));
+    // Rows [j0, j0 + n) of this (sequence, kv head), contiguous in both
+    // layouts (a page holds whole chunks); loads past them return 0, and so
+    // do all of them for a page id outside the pool.
+    const int64_t off = rows.offset(b, Hkv, kvh, j0);
+    const int nbytes = off < 0 ? 0 : n * kHeadDim * (int)sizeof(T);
+    const __amdgpu_buffer_rsrc_t rk = make_rsrc(kc + (off < 0 ? 0 : off), nbytes);
+    const __amdgpu_buffer_rsrc_t rv = make_rsrc(vc + (off < 0 ? 0 : off), nbytes);
     constexpr int kRowBytes = kHeadDim * (int)sizeof(T);
 
 #if CRANE_DECODE_EARLYV
@@ -367,9 +370,9 @@ __device__ __forceinline__ void decode_item(
 // the slowest grid dimension, so every sequence's first chunks go first and the
 // workgroups past the shorter sequences' ends (which exit at once) come last
 // instead of being interleaved.  grid: (groups * kCL, B, ceil(nsplit / kCL)).
-template <typename T, int G>
+template <typename T, int G, class ROWS>
 __global__ __launch_bounds__(kThreads) void decode_chunk_kernel(
-    const T* __restrict__ q, const T* __restrict__ kc, const T* __restrict__ vc, int64_t cap,
+    const T* __restrict__ q, const T* __restrict__ kc, const T* __restrict__ vc, ROWS rows,
     const int32_t* __restrict__ kv_len, int max_kv, int Hq, int Hkv, int n_rep, float scale, int nsplit,
     float* __restrict__ ws_o, float* __restrict__ ws_ml, T* __restrict__ out) {
     __shared__ DecodeShared<T, G> sm;
@@ -377,8 +380,8 @@ __global__ __launch_bounds__(kThreads) void decode_chunk_kernel(
     if (c >= nsplit) return;
     const int b = blockIdx.y;
     const int L = min(kv_len[b], max_kv);  // never read past the rows the host vouched for
-    decode_item<T, G>(sm, q, kc, vc, cap, L, b, blockIdx.x / kCL, c, Hq, Hkv, n_rep, scale, nsplit, ws_o, ws_ml,
-                      out);
+    decode_item<T, G, ROWS>(sm, q, kc, vc, rows, L, b, blockIdx.x / kCL, c, Hq, Hkv, n_rep, scale, nsplit, ws_o,
+                            ws_ml, out);
 }
 
 // Kernel 2: log-sum-exp merge of one (sequence, q head)'s partials; thread d
@@ -446,27 +449,27 @@ int pick_group(int n_rep) {
     return 1;
 }
 
-template <typename T, int G>
-int launch_decode_g(const T* q, const T* kc, const T* vc, int64_t cap, const int32_t* kv_len, int max_kv,
+template <typename T, int G, class ROWS>
+int launch_decode_g(const T* q, const T* kc, const T* vc, const ROWS& rows, const int32_t* kv_len, int max_kv,
                     int nsplit, int B, int Hq, int Hkv, float scale, float* ws_o, float* ws_ml, T* out,
                     hipStream_t st) {
     const int n_rep = Hq / Hkv;
     const int groups = Hkv * (n_rep / G);
     const dim3 grid((unsigned)(groups * kCL), (unsigned)B, (unsigned)((nsplit + kCL - 1) / kCL));
-    hipLaunchKernelGGL((decode_chunk_kernel<T, G>), grid, dim3(kThreads), 0, st, q, kc, vc, cap, kv_len, max_kv,
+    hipLaunchKernelGGL((decode_chunk_kernel<T, G, ROWS>), grid, dim3(kThreads), 0, st, q, kc, vc, rows, kv_len, max_kv,
                        Hq, Hkv, n_rep, scale, nsplit, ws_o, ws_ml, out);
     return hipGetLastError() == hipSuccess ? CRANE_HIP_OK : CRANE_HIP_E_LAUNCH;
 }
 
-template <typename T>
-int launch_decode(const T* q, const T* kc, const T* vc, int64_t cap, const int32_t* kv_len, int max_kv, int nsplit,
+template <typename T, class ROWS>
+int launch_decode(const T* q, const T* kc, const T* vc, const ROWS& rows, const int32_t* kv_len, int max_kv, int nsplit,
                   int B, int Hq, int Hkv, float scale, float* ws_o, float* ws_ml, T* out, hipStream_t st) {
     int rc;
     switch (pick_group(Hq / Hkv)) {
 #define CRANE_DECODE_CASE(g)                                                                                      \
     case g:                                                                                                       \
-        rc = launch_decode_g<T, g>(q, kc, vc, cap, kv_len, max_kv, nsplit, B, Hq, Hkv, scale, ws_o, ws_ml, out,  \
-                                   st);                                                                           \
+        rc = launch_decode_g<T, g, ROWS>(q, kc, vc, rows, kv_len, max_kv, nsplit, B, Hq, Hkv, scale, ws_o, ws_ml, \
+                                         out, st);                                                                \
         break;
         CRANE_DECODE_CASE(1)
         CRANE_DECODE_CASE(2)
@@ -502,6 +505,35 @@ WsLayout ws_layout(int B, int Hq, int64_t ns) {
     return w;
 }
 
+// Checks shared by both layouts, then the launch; `rows` addresses the cache.
+template <class ROWS>
+int attn_decode(const void* q, const void* k_cache, const void* v_cache, const ROWS& rows, const int32_t* kv_len,
+                int64_t max_kv, int B, int Hq, int Hkv, int D, float scale, void* workspace, size_t ws_bytes,
+                void* out, int dtype, void* stream) {
+    if (dtype != CRANE_HIP_F32 && dtype != CRANE_HIP_BF16) return CRANE_HIP_E_DTYPE;
+    if (D != kHeadDim) return CRANE_HIP_E_HEAD_DIM;
+    if (B < 0 || Hq <= 0 || Hkv <= 0) return CRANE_HIP_E_INVALID;
+    if (Hq % Hkv != 0) return CRANE_HIP_E_GQA;
+    if (max_kv <= 0) return CRANE_HIP_E_INVALID;
+    if (!(scale > 0.0f) || !__builtin_isfinite(scale)) return CRANE_HIP_E_INVALID;
+    if (B == 0) return CRANE_HIP_OK;
+    if (!q || !k_cache || !v_cache || !kv_len || !out) return CRANE_HIP_E_INVALID;
+    if (!aligned16(q) || !aligned16(k_cache) || !aligned16(v_cache)) return CRANE_HIP_E_ALIGN;
+    const int64_t ns = n_splits(max_kv);
+    if (max_kv > 0x7fffffffLL || ns > kMaxSplits || B > 65535 || (int64_t)B * Hq > 0x7fffffffLL)
+        return CRANE_HIP_E_INVALID;
+    const WsLayout w = ws_layout(B, Hq, ns);
+    if (!workspace || ws_bytes < w.total || !aligned16(workspace)) return CRANE_HIP_E_WORKSPACE;
+    float* ws_o = (float*)((char*)workspace + w.o_off);
+    float* ws_ml = (float*)((char*)workspace + w.ml_off);
+    hipStream_t st = (hipStream_t)stream;
+    if (dtype == CRANE_HIP_F32)
+        return launch_decode<float>((const float*)q, (const float*)k_cache, (const float*)v_cache, rows, kv_len,
+                                    (int)max_kv, (int)ns, B, Hq, Hkv, scale, ws_o, ws_ml, (float*)out, st);
+    return launch_decode<bf16_t>((const bf16_t*)q, (const bf16_t*)k_cache, (const bf16_t*)v_cache, rows, kv_len,
+                                 (int)max_kv, (int)ns, B, Hq, Hkv, scale, ws_o, ws_ml, (bf16_t*)out, st);
+}
+
 }  // namespace
 }  // namespace crane
 
@@ -517,27 +549,19 @@ extern "C" int crane_hip_attn_decode(const void* q, const void* k_cache, const v
                                      const int32_t* kv_len, int64_t max_kv, int B, int Hq, int Hkv, int D,
                                      float scale, void* workspace, size_t ws_bytes, void* out, int dtype,
                                      void* stream) {
-    if (dtype != CRANE_HIP_F32 && dtype != CRANE_HIP_BF16) return CRANE_HIP_E_DTYPE;
-    if (D != kHeadDim) return CRANE_HIP_E_HEAD_DIM;
-    if (B < 0 || Hq <= 0 || Hkv <= 0) return CRANE_HIP_E_INVALID;
-    if (Hq % Hkv != 0) return CRANE_HIP_E_GQA;
     if (cache_cap <= 0 || max_kv > cache_cap) return CRANE_HIP_E_CAPACITY;
-    if (max_kv <= 0) return CRANE_HIP_E_INVALID;
-    if (!(scale > 0.0f) || !__builtin_isfinite(scale)) return CRANE_HIP_E_INVALID;
-    if (B == 0) return CRANE_HIP_OK;
-    if (!q || !k_cache || !v_cache || !kv_len || !out) return CRANE_HIP_E_INVALID;
-    if (!aligned16(q) || !aligned16(k_cache) || !aligned16(v_cache)) return CRANE_HIP_E_ALIGN;
-    const int64_t ns = n_splits(max_kv);
-    if (max_kv > 0x7fffffffLL || ns > kMaxSplits || B > 65535 || (int64_t)B * Hq > 0x7fffffffLL)
-        return CRANE_HIP_E_INVALID;
-    const WsLayout w = ws_layout(B, Hq, ns);
-    if (!workspace || ws_bytes < w.total || !aligned16(workspace)) return CRANE_HIP_E_WORKSPACE;
-    float* ws_o = (float*)((char*)workspace + w.o_off);
-    float* ws_ml = (float*)((char*)workspace + w.ml_off);
-    hipStream_t st = (hipStream_t)stream;
-    if (dtype == CRANE_HIP_F32)
-        return launch_decode<float>((const float*)q, (const float*)k_cache, (const float*)v_cache, cache_cap, kv_len,
-                                    (int)max_kv, (int)ns, B, Hq, Hkv, scale, ws_o, ws_ml, (float*)out, st);
-    return launch_decode<bf16_t>((const bf16_t*)q, (const bf16_t*)k_cache, (const bf16_t*)v_cache, cache_cap,
-                                 kv_len, (int)max_kv, (int)ns, B, Hq, Hkv, scale, ws_o, ws_ml, (bf16_t*)out, st);
+    return attn_decode(q, k_cache, v_cache, DenseRows{cache_cap}, kv_len, max_kv, B, Hq, Hkv, D, scale, workspace,
+                       ws_bytes, out, dtype, stream);
+}
+
+extern "C" int crane_hip_attn_decode_paged(const void* q, const void* k_pool, const void* v_pool, int64_t n_pages,
+                                           int page_rows, const int32_t* block_table, int64_t table_stride,
+                                           const int32_t* kv_len, int64_t max_kv, int B, int Hq, int Hkv, int D,
+                                           float scale, void* workspace, size_t ws_bytes, void* out, int dtype,
+                                           void* stream) {
+    const int rc = check_paged(n_pages, page_rows, block_table, table_stride, Hkv);
+    if (rc) return rc;
+    if (max_kv > table_stride * page_rows) return CRANE_HIP_E_CAPACITY;
+    return attn_decode(q, k_pool, v_pool, PagedRows{block_table, table_stride, n_pages, page_rows}, kv_len, max_kv, B,
+                       Hq, Hkv, D, scale, workspace, ws_bytes, out, dtype, stream);
 }

@@ -151,9 +151,9 @@ __device__ __forceinline__ bool map_block(int id, int n_qt, int B, int Hkv, int 
     return true;
 }
 
-template <bool CAUSAL>
+template <bool CAUSAL, class ROWS>
 __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(2, 2))) void prefill_bf16_kernel(
-    const bf16_t* __restrict__ q, const bf16_t* __restrict__ kc, const bf16_t* __restrict__ vc, int64_t cap,
+    const bf16_t* __restrict__ q, const bf16_t* __restrict__ kc, const bf16_t* __restrict__ vc, ROWS rows,
     const int32_t* __restrict__ start_pos, int max_start, int S, int B, int Hq, int Hkv, float scale_log2,
     bf16_t* __restrict__ out) {
     const int n_rep = Hq / Hkv;
@@ -177,15 +177,30 @@ __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(2, 
     const int L = start + S;                                 // cache rows holding keys for this chunk
     const int kend = CAUSAL ? min(start + m0 + kBM, L) : L;  // keys any row of the tile can see
     const int n_tiles = (kend + kBN - 1) / kBN;
-    const int64_t head0 = ((int64_t)b * Hkv + kvh) * cap * kHeadDim;
-    const __amdgpu_buffer_rsrc_t rk = make_rsrc(kc + head0, L * kHeadDim * 2);
-    const __amdgpu_buffer_rsrc_t rv = make_rsrc(vc + head0, L * kHeadDim * 2);
     uint32_t vofs[kCopies];
 #pragma unroll
     for (int i = 0; i < kCopies; ++i) vofs[i] = pinned(copy_voffset(i, wave, lane));
-    issue_tile(rk, 0, wave, vofs, kbuf[0]);
-    issue_tile(rv, 0, wave, vofs, vbuf[0]);
-    if (n_tiles > 1) issue_tile(rk, 1, wave, vofs, kbuf[1]);
+    // Tile x of K (or V) into LDS.  Dense: one resource over the sequence's L
+    // rows, the tile picked by the scalar offset.  Paged: a resource over the
+    // tile's rows inside its page (a page holds whole tiles); rows past L, and
+    // a page id outside the pool, read as zero.
+    const int64_t head0 = ROWS::kPaged ? 0 : rows.offset(b, Hkv, kvh, 0);
+    const __amdgpu_buffer_rsrc_t rk = make_rsrc(kc + head0, L * kHeadDim * 2);
+    const __amdgpu_buffer_rsrc_t rv = make_rsrc(vc + head0, L * kHeadDim * 2);
+    auto issue = [&](const bf16_t* pool, const __amdgpu_buffer_rsrc_t& whole, int x, uint8_t* dst)
+        __attribute__((always_inline)) {
+        if constexpr (ROWS::kPaged) {
+            const int key0 = x * kBN;
+            const int64_t off = key0 < L ? rows.offset(b, Hkv, kvh, key0) : -1;
+            const int bytes = off < 0 ? 0 : min(kBN, L - key0) * kHeadDim * 2;
+            issue_tile(make_rsrc(pool + (off < 0 ? 0 : off), bytes), 0, wave, vofs, dst);
+        } else {
+            issue_tile(whole, x, wave, vofs, dst);
+        }
+    };
+    issue(kc, rk, 0, kbuf[0]);
+    issue(vc, rv, 0, vbuf[0]);
+    if (n_tiles > 1) issue(kc, rk, 1, kbuf[1]);
 
     // Q fragments (B operand of S^T = K Q^T): query row qrow, dims 16ks + 8hh .. +7.
     const int qrow = m0 + wave * 32 + n;
@@ -242,8 +257,8 @@ __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(2, 
         constexpr int par = decltype(parity)::value;
         CRANE_WAIT_VMCNT(0);  // this wave's copies of V(t) and K(t+1) have landed
         __syncthreads();      // ... and every wave's; K(t) and V(t-1) are fully consumed
-        if (t + 2 < n_tiles) issue_tile(rk, t + 2, wave, vofs, kbuf[par]);
-        if (t + 1 < n_tiles) issue_tile(rv, t + 1, wave, vofs, vbuf[par ^ 1]);
+        if (t + 2 < n_tiles) issue(kc, rk, t + 2, kbuf[par]);
+        if (t + 1 < n_tiles) issue(vc, rv, t + 1, vbuf[par ^ 1]);
         const int kt = t * kBN;
         if (CAUSAL && kt > wave_first + 31) return;  // the whole tile is above this wave's diagonal
         if (kt + kBN > kend || (CAUSAL && kt + kBN - 1 > wave_first)) {  // diagonal or last tile
@@ -341,9 +356,9 @@ __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(2, 
 }
 
 // f32: one wave per (query row, q head, sequence); lane owns dims 2*lane, 2*lane+1.
-template <bool CAUSAL>
+template <bool CAUSAL, class ROWS>
 __global__ __launch_bounds__(64) void prefill_f32_kernel(const float* __restrict__ q, const float* __restrict__ kc,
-                                                         const float* __restrict__ vc, int64_t cap,
+                                                         const float* __restrict__ vc, ROWS rows,
                                                          const int32_t* __restrict__ start_pos, int max_start, int S,
                                                          int Hq, int Hkv, float scale_log2, float* __restrict__ out) {
     const int i = blockIdx.x, hq = blockIdx.y, b = blockIdx.z;
@@ -353,18 +368,17 @@ __global__ __launch_bounds__(64) void prefill_f32_kernel(const float* __restrict
     const int L = start + S;
     const int kend = CAUSAL ? start + i + 1 : L;
     const float2 qv = *reinterpret_cast<const float2*>(q + (((int64_t)b * Hq + hq) * S + i) * kHeadDim + 2 * lane);
-    const float* Kg = kc + ((int64_t)b * Hkv + kvh) * cap * kHeadDim + 2 * lane;
-    const float* Vg = vc + ((int64_t)b * Hkv + kvh) * cap * kHeadDim + 2 * lane;
     float m = -INFINITY, l = 0.f, o0 = 0.f, o1 = 0.f;
     for (int j = 0; j < kend; ++j) {
-        const float2 kv = *reinterpret_cast<const float2*>(Kg + (int64_t)j * kHeadDim);
+        const int64_t off = rows.offset(b, Hkv, kvh, j);  // a row on an invalid page reads as zero
+        const float2 kv = off < 0 ? make_float2(0.f, 0.f) : *reinterpret_cast<const float2*>(kc + off + 2 * lane);
         float s = qv.x * kv.x + qv.y * kv.y;
 #pragma unroll
         for (int msk = 32; msk >= 1; msk >>= 1) s += __shfl_xor(s, msk);
         s *= scale_log2;
         const float m_new = fmaxf(m, s);
         const float alpha = fast_exp2(m - m_new), p = fast_exp2(s - m_new);
-        const float2 vv = *reinterpret_cast<const float2*>(Vg + (int64_t)j * kHeadDim);
+        const float2 vv = off < 0 ? make_float2(0.f, 0.f) : *reinterpret_cast<const float2*>(vc + off + 2 * lane);
         l = l * alpha + p;
         o0 = o0 * alpha + p * vv.x;
         o1 = o1 * alpha + p * vv.y;
@@ -372,6 +386,53 @@ __global__ __launch_bounds__(64) void prefill_f32_kernel(const float* __restrict
     }
     float* op = out + (((int64_t)b * S + i) * Hq + hq) * kHeadDim + 2 * lane;
     *reinterpret_cast<float2*>(op) = make_float2(o0 / l, o1 / l);
+}
+
+// Checks shared by both layouts, then the launch; `rows` addresses the cache.
+template <class ROWS>
+int attn_prefill(const void* q, const void* k_cache, const void* v_cache, const ROWS& rows, const int32_t* start_pos,
+                 int64_t max_start, int B, int S, int Hq, int Hkv, int D, float scale, int causal, void* out,
+                 int dtype, void* stream) {
+    if (dtype != CRANE_HIP_F32 && dtype != CRANE_HIP_BF16) return CRANE_HIP_E_DTYPE;
+    if (D != kHeadDim) return CRANE_HIP_E_HEAD_DIM;
+    if (B < 0 || S < 0 || Hq <= 0 || Hkv <= 0 || max_start < 0) return CRANE_HIP_E_INVALID;
+    if (Hq % Hkv != 0) return CRANE_HIP_E_GQA;
+    if (!(scale > 0.0f) || !__builtin_isfinite(scale)) return CRANE_HIP_E_INVALID;
+    if (B == 0 || S == 0) return CRANE_HIP_OK;
+    if (!q || !k_cache || !v_cache || !start_pos || !out) return CRANE_HIP_E_INVALID;
+    if (!aligned16(q) || !aligned16(k_cache) || !aligned16(v_cache) || !aligned16(out)) return CRANE_HIP_E_ALIGN;
+    if (max_start + (int64_t)S > 0x7fffffffLL / (kHeadDim * 4) || B > 65535 || Hq > 65535) return CRANE_HIP_E_INVALID;
+    hipStream_t st = (hipStream_t)stream;
+    if (dtype == CRANE_HIP_BF16) {
+        // candle scales the bf16 scores by the scale converted to bf16 (affine in T)
+        const float sl = host_round_bf16(scale) * kLog2e;
+        const int n_rep = Hq / Hkv;
+        const int64_t n_qt = (S + kBM - 1) / kBM;
+        const int64_t units = n_qt * B * Hkv;
+        const int64_t chunk = 8LL * n_rep;
+        const int64_t blocks = ((units + 7) / 8) * chunk;
+        if (blocks > 0x7fffffffLL) return CRANE_HIP_E_INVALID;
+        if (causal)
+            hipLaunchKernelGGL((prefill_bf16_kernel<true, ROWS>), dim3((unsigned)blocks), dim3(64 * kWaves), 0, st,
+                               (const bf16_t*)q, (const bf16_t*)k_cache, (const bf16_t*)v_cache, rows, start_pos,
+                               (int)max_start, S, B, Hq, Hkv, sl, (bf16_t*)out);
+        else
+            hipLaunchKernelGGL((prefill_bf16_kernel<false, ROWS>), dim3((unsigned)blocks), dim3(64 * kWaves), 0, st,
+                               (const bf16_t*)q, (const bf16_t*)k_cache, (const bf16_t*)v_cache, rows, start_pos,
+                               (int)max_start, S, B, Hq, Hkv, sl, (bf16_t*)out);
+    } else {
+        const float sl = scale * kLog2e;
+        const dim3 grid((unsigned)S, (unsigned)Hq, (unsigned)B);
+        if (causal)
+            hipLaunchKernelGGL((prefill_f32_kernel<true, ROWS>), grid, dim3(64), 0, st, (const float*)q,
+                               (const float*)k_cache, (const float*)v_cache, rows, start_pos, (int)max_start, S, Hq,
+                               Hkv, sl, (float*)out);
+        else
+            hipLaunchKernelGGL((prefill_f32_kernel<false, ROWS>), grid, dim3(64), 0, st, (const float*)q,
+                               (const float*)k_cache, (const float*)v_cache, rows, start_pos, (int)max_start, S, Hq,
+                               Hkv, sl, (float*)out);
+    }
+    return launch_status(hipGetLastError());
 }
 
 }  // namespace
@@ -384,43 +445,21 @@ extern "C" int crane_hip_attn_prefill(const void* q, const void* k_cache, const 
                                       int D, float scale, int causal, void* out, int dtype, void* stream) {
     if (dtype != CRANE_HIP_F32 && dtype != CRANE_HIP_BF16) return CRANE_HIP_E_DTYPE;
     if (D != kHeadDim) return CRANE_HIP_E_HEAD_DIM;
-    if (B < 0 || S < 0 || Hq <= 0 || Hkv <= 0 || max_start < 0) return CRANE_HIP_E_INVALID;
-    if (Hq % Hkv != 0) return CRANE_HIP_E_GQA;
-    if (!(scale > 0.0f) || !__builtin_isfinite(scale)) return CRANE_HIP_E_INVALID;
+    if (max_start < 0 || S < 0) return CRANE_HIP_E_INVALID;
     if (cache_cap <= 0 || max_start + (int64_t)S > cache_cap) return CRANE_HIP_E_CAPACITY;
-    if (B == 0 || S == 0) return CRANE_HIP_OK;
-    if (!q || !k_cache || !v_cache || !start_pos || !out) return CRANE_HIP_E_INVALID;
-    if (!aligned16(q) || !aligned16(k_cache) || !aligned16(v_cache) || !aligned16(out)) return CRANE_HIP_E_ALIGN;
-    if (cache_cap > 0x7fffffffLL || B > 65535 || Hq > 65535) return CRANE_HIP_E_INVALID;
-    hipStream_t st = (hipStream_t)stream;
-    if (dtype == CRANE_HIP_BF16) {
-        // candle scales the bf16 scores by the scale converted to bf16 (affine in T)
-        const float sl = host_round_bf16(scale) * kLog2e;
-        const int n_rep = Hq / Hkv;
-        const int64_t n_qt = (S + kBM - 1) / kBM;
-        const int64_t units = n_qt * B * Hkv;
-        const int64_t chunk = 8LL * n_rep;
-        const int64_t blocks = ((units + 7) / 8) * chunk;
-        if (blocks > 0x7fffffffLL) return CRANE_HIP_E_INVALID;
-        if (causal)
-            hipLaunchKernelGGL(prefill_bf16_kernel<true>, dim3((unsigned)blocks), dim3(64 * kWaves), 0, st,
-                               (const bf16_t*)q, (const bf16_t*)k_cache, (const bf16_t*)v_cache, cache_cap, start_pos,
-                               (int)max_start, S, B, Hq, Hkv, sl, (bf16_t*)out);
-        else
-            hipLaunchKernelGGL(prefill_bf16_kernel<false>, dim3((unsigned)blocks), dim3(64 * kWaves), 0, st,
-                               (const bf16_t*)q, (const bf16_t*)k_cache, (const bf16_t*)v_cache, cache_cap, start_pos,
-                               (int)max_start, S, B, Hq, Hkv, sl, (bf16_t*)out);
-    } else {
-        const float sl = scale * kLog2e;
-        const dim3 grid((unsigned)S, (unsigned)Hq, (unsigned)B);
-        if (causal)
-            hipLaunchKernelGGL(prefill_f32_kernel<true>, grid, dim3(64), 0, st, (const float*)q, (const float*)k_cache,
-                               (const float*)v_cache, cache_cap, start_pos, (int)max_start, S, Hq, Hkv, sl,
-                               (float*)out);
-        else
-            hipLaunchKernelGGL(prefill_f32_kernel<false>, grid, dim3(64), 0, st, (const float*)q,
-                               (const float*)k_cache, (const float*)v_cache, cache_cap, start_pos, (int)max_start, S,
-                               Hq, Hkv, sl, (float*)out);
-    }
-    return launch_status(hipGetLastError());
+    if (cache_cap > 0x7fffffffLL) return CRANE_HIP_E_INVALID;
+    return attn_prefill(q, k_cache, v_cache, DenseRows{cache_cap}, start_pos, max_start, B, S, Hq, Hkv, D, scale,
+                        causal, out, dtype, stream);
+}
+
+extern "C" int crane_hip_attn_prefill_paged(const void* q, const void* k_pool, const void* v_pool, int64_t n_pages,
+                                            int page_rows, const int32_t* block_table, int64_t table_stride,
+                                            const int32_t* start_pos, int64_t max_start, int B, int S, int Hq, int Hkv,
+                                            int D, float scale, int causal, void* out, int dtype, void* stream) {
+    const int rc = check_paged(n_pages, page_rows, block_table, table_stride, Hkv);
+    if (rc) return rc;
+    if (max_start < 0 || S < 0) return CRANE_HIP_E_INVALID;
+    if (max_start + (int64_t)S > table_stride * page_rows) return CRANE_HIP_E_CAPACITY;
+    return attn_prefill(q, k_pool, v_pool, PagedRows{block_table, table_stride, n_pages, page_rows}, start_pos,
+                        max_start, B, S, Hq, Hkv, D, scale, causal, out, dtype, stream);
 }

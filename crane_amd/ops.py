@@ -223,3 +223,111 @@ def attention_prefill(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Ten
         max_start, B, S, Hq, k_cache.shape[1], D, scale, int(bool(causal)), out.data_ptr(), dt, _stream(dev))
     check(rc, "attention_prefill")
     return out
+
+
+# ------------------------------------------------------------- paged layout
+# K and V pools [n_pages, Hkv, page_rows, D] and a block table [B, stride]
+# (int32): row j of sequence b is row j % page_rows of page
+# block_table[b, j // page_rows].  Same operations, same results as the dense
+# entry points over the same rows (include/crane_hip.h, paged launchers).
+
+PAGE_ALIGN = 256
+
+
+def _paged_args(k_pool: torch.Tensor, v_pool: torch.Tensor, block_table: torch.Tensor, B: int,
+                dtype: torch.dtype):
+    if k_pool.shape != v_pool.shape or k_pool.dim() != 4 or k_pool.shape[3] != HEAD_DIM:
+        raise CraneHipError(_lib.E_INVALID, "pools must be [n_pages, Hkv, page_rows, D]")
+    for t, name in ((k_pool, "k_pool"), (v_pool, "v_pool")):
+        _contig(t, name)
+        if t.dtype != dtype:
+            raise CraneHipError(_lib.E_DTYPE, f"{name} dtype {t.dtype} != {dtype}")
+    if block_table.dtype != torch.int32 or block_table.dim() != 2 or block_table.shape[0] != B or \
+            not block_table.is_contiguous():
+        raise CraneHipError(_lib.E_INVALID, "block_table must be a contiguous int32 [B, max_pages] tensor")
+    n_pages, Hkv, page_rows, _ = k_pool.shape
+    return n_pages, Hkv, page_rows, block_table.shape[1]
+
+
+def qk_norm_rope_append_paged(qkv: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, positions: torch.Tensor,
+                              k_pool: torch.Tensor, v_pool: torch.Tensor, block_table: torch.Tensor,
+                              cache_len: torch.Tensor, num_heads: int, q_norm_w: Optional[torch.Tensor] = None,
+                              k_norm_w: Optional[torch.Tensor] = None, eps: float = 1e-6,
+                              order: str = "norm_then_rope") -> torch.Tensor:
+    """qk_norm_rope_append into a paged cache: token s of sequence b lands in
+    its row cache_len[b]+s.  Returns q [B, Hq, S, D]."""
+    dev = _dev(qkv, cos, sin, positions, k_pool, v_pool, block_table, cache_len, q_norm_w, k_norm_w)
+    if qkv.dim() != 3:
+        raise CraneHipError(_lib.E_INVALID, "qkv must be [B, S, (Hq+2Hkv)*D]")
+    B, S, W = qkv.shape
+    n_pages, Hkv, page_rows, stride = _paged_args(k_pool, v_pool, block_table, B, qkv.dtype)
+    if W != (num_heads + 2 * Hkv) * HEAD_DIM:
+        raise CraneHipError(_lib.E_INVALID, f"qkv last dim {W} != (Hq+2Hkv)*{HEAD_DIM}")
+    dt = _dtype_code(qkv)
+    for t, name in ((cos, "cos"), (sin, "sin"), (q_norm_w, "q_norm_w"), (k_norm_w, "k_norm_w")):
+        if t is not None and t.dtype != qkv.dtype:
+            raise CraneHipError(_lib.E_DTYPE, f"{name} dtype {t.dtype} != qkv dtype {qkv.dtype}")
+    if qkv.stride(2) != 1 or qkv.stride(0) != S * qkv.stride(1):
+        raise CraneHipError(_lib.E_INVALID, "qkv rows must be dense with a unit inner stride")
+    _contig(cos, "cos")
+    _contig(sin, "sin")
+    if cos.shape != sin.shape or cos.dim() != 2 or cos.shape[1] != HEAD_DIM // 2:
+        raise CraneHipError(_lib.E_INVALID, "cos/sin must be [max_pos, D/2]")
+    _i32(positions, B, "positions")
+    _i32(cache_len, B, "cache_len")
+    if order not in _ORDERS:
+        raise CraneHipError(_lib.E_INVALID, f"order {order!r}")
+    q_out = torch.empty((B, num_heads, S, HEAD_DIM), dtype=qkv.dtype, device=dev)
+    rc = _lib.lib().crane_hip_qknorm_rope_append_paged(
+        qkv.data_ptr(), qkv.stride(1), _ptr(q_norm_w), _ptr(k_norm_w), eps, _ORDERS[order], cos.data_ptr(),
+        sin.data_ptr(), cos.stride(0), cos.shape[0], positions.data_ptr(), q_out.data_ptr(), k_pool.data_ptr(),
+        v_pool.data_ptr(), n_pages, page_rows, block_table.data_ptr(), stride, cache_len.data_ptr(), B, S,
+        num_heads, Hkv, HEAD_DIM, dt, _stream(dev))
+    check(rc, "qk_norm_rope_append_paged")
+    return q_out
+
+
+def attention_decode_paged(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tensor, block_table: torch.Tensor,
+                           kv_len: torch.Tensor, max_kv: int, scale: Optional[float] = None,
+                           workspace: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """attention_decode over a paged cache: q [B, Hq, D]; [B, 1, Hq*D]."""
+    dev = _dev(q, k_pool, v_pool, block_table, kv_len, workspace)
+    if q.dim() != 3 or q.shape[2] != HEAD_DIM:
+        raise CraneHipError(_lib.E_INVALID, "q must be [B, Hq, 128]")
+    B, Hq, D = q.shape
+    n_pages, Hkv, page_rows, stride = _paged_args(k_pool, v_pool, block_table, B, q.dtype)
+    _contig(q, "q")
+    dt = _dtype_code(q)
+    _i32(kv_len, B, "kv_len")
+    scale = 1.0 / math.sqrt(D) if scale is None else float(scale)
+    if workspace is None:
+        workspace = decode_workspace(dev, decode_workspace_bytes(B, Hq, Hkv, max_kv, q.dtype))
+    out = torch.empty((B, 1, Hq * D), dtype=q.dtype, device=dev)
+    rc = _lib.lib().crane_hip_attn_decode_paged(
+        q.data_ptr(), k_pool.data_ptr(), v_pool.data_ptr(), n_pages, page_rows, block_table.data_ptr(), stride,
+        kv_len.data_ptr(), max_kv, B, Hq, Hkv, D, scale, workspace.data_ptr(),
+        workspace.numel() * workspace.element_size(), out.data_ptr(), dt, _stream(dev))
+    check(rc, "attention_decode_paged")
+    return out
+
+
+def attention_prefill_paged(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tensor,
+                            block_table: torch.Tensor, start_pos: torch.Tensor, max_start: int,
+                            scale: Optional[float] = None, causal: bool = True) -> torch.Tensor:
+    """attention_prefill over a paged cache: q [B, Hq, S, D]; [B, S, Hq*D]."""
+    dev = _dev(q, k_pool, v_pool, block_table, start_pos)
+    if q.dim() != 4 or q.shape[3] != HEAD_DIM:
+        raise CraneHipError(_lib.E_INVALID, "q must be [B, Hq, S, 128]")
+    B, Hq, S, D = q.shape
+    n_pages, Hkv, page_rows, stride = _paged_args(k_pool, v_pool, block_table, B, q.dtype)
+    _contig(q, "q")
+    dt = _dtype_code(q)
+    _i32(start_pos, B, "start_pos")
+    scale = 1.0 / math.sqrt(D) if scale is None else float(scale)
+    out = torch.empty((B, S, Hq * D), dtype=q.dtype, device=dev)
+    rc = _lib.lib().crane_hip_attn_prefill_paged(
+        q.data_ptr(), k_pool.data_ptr(), v_pool.data_ptr(), n_pages, page_rows, block_table.data_ptr(), stride,
+        start_pos.data_ptr(), max_start, B, S, Hq, Hkv, D, scale, int(bool(causal)), out.data_ptr(), dt,
+        _stream(dev))
+    check(rc, "attention_prefill_paged")
+    return out

@@ -134,6 +134,54 @@ int crane_hip_attn_prefill(const void* q, const void* k_cache, const void* v_cac
                            int B, int S, int Hq, int Hkv, int D, float scale, int causal,
                            void* out, int dtype, void* stream);
 
+/* ---- Paged KV cache ------------------------------------------------------
+ *
+ * The same three operations over a paged cache: K and V pools
+ * [n_pages, Hkv, page_rows, D] (rows of D contiguous, as in Crane's layout)
+ * and a block table (int32, device) of `table_stride` page ids per sequence.
+ * Row j of sequence b is row j % page_rows of page
+ * block_table[b * table_stride + j / page_rows]; a sequence holds at most
+ * table_stride * page_rows rows.  page_rows is a positive multiple of
+ * CRANE_HIP_PAGE_ALIGN (a decode work item then never straddles a page).  A
+ * page id outside [0, n_pages) is never dereferenced: its rows read as zeros
+ * and are not written.
+ *
+ * Sequences keep their rows where they were appended, so batched decode reads
+ * every sequence in place, a batch is a set of table rows, and growth is a new
+ * page id.  This replaces the per-round KV copies of Crane's batched decode
+ * (setup_batch_decode + pad_and_stack_kv_caches, qwen3/modeling.rs:973-1030,
+ * 1141-1200; extract_batch_kv :1066-1102) and the reallocation copy of
+ * update_kv_cache when a buffer is full (:333-355).  Arguments not described
+ * here mean what they mean for the dense launchers above; the decode workspace
+ * is sized by crane_hip_attn_decode_workspace. */
+#define CRANE_HIP_PAGE_ALIGN 256
+
+/* crane_hip_qknorm_rope_append into the pools: token s of sequence b lands in
+ * row cache_len[b]+s of that sequence (a row past its capacity or on an
+ * invalid page is not written). */
+int crane_hip_qknorm_rope_append_paged(const void* qkv, int64_t qkv_row_stride,
+                                       const void* q_norm_w, const void* k_norm_w, float eps,
+                                       int order, const void* cos, const void* sin, int64_t cs_stride,
+                                       int64_t table_rows, const int32_t* positions, void* q_out,
+                                       void* k_pool, void* v_pool, int64_t n_pages, int page_rows,
+                                       const int32_t* block_table, int64_t table_stride,
+                                       const int32_t* cache_len, int B, int S, int Hq, int Hkv, int D,
+                                       int dtype, void* stream);
+
+/* crane_hip_attn_decode over the pools (max_kv <= table_stride * page_rows). */
+int crane_hip_attn_decode_paged(const void* q, const void* k_pool, const void* v_pool,
+                                int64_t n_pages, int page_rows, const int32_t* block_table,
+                                int64_t table_stride, const int32_t* kv_len, int64_t max_kv, int B,
+                                int Hq, int Hkv, int D, float scale, void* workspace,
+                                size_t ws_bytes, void* out, int dtype, void* stream);
+
+/* crane_hip_attn_prefill over the pools (max_start + S <= table_stride * page_rows). */
+int crane_hip_attn_prefill_paged(const void* q, const void* k_pool, const void* v_pool,
+                                 int64_t n_pages, int page_rows, const int32_t* block_table,
+                                 int64_t table_stride, const int32_t* start_pos, int64_t max_start,
+                                 int B, int S, int Hq, int Hkv, int D, float scale, int causal,
+                                 void* out, int dtype, void* stream);
+
 /* Library and kernel-build identification, e.g. "crane_hip 1 gfx950". */
 const char* crane_hip_version(void);
 
