@@ -248,6 +248,50 @@ def bench_decode_paged(args, dev, stream, lib):
     return dict(ms=ms, gbs=gbs, page_rows=P, n_pages=n_pages)
 
 
+def bench_layer(args, dev, stream, lib):
+    """The decoder-layer row kernels (include/crane_layer.h) at config 4's
+    prefill rows (Qwen2.5-7B: 8 x 4096 rows, hidden 3584, intermediate 18944)
+    and config 3's decode rows (Qwen3-8B: 32 rows, hidden 4096, intermediate
+    12288).  Algorithmic bytes: every tensor read or written once (the norm
+    weight counted once)."""
+    import torch
+    res = {}
+    st = stream.cuda_stream
+    for tag, rows, hidden, inter in (("c4_prefill_rows", 8 * 4096, 3584, 18944), ("c3_decode_rows", 32, 4096, 12288)):
+        gen = torch.Generator(device=dev).manual_seed(SEED0 + 7)
+        x = randn((rows, hidden), gen, torch.bfloat16, dev)
+        h = randn((rows, hidden), gen, torch.bfloat16, dev)
+        w = randn((hidden,), gen, torch.bfloat16, dev)
+        out = torch.empty_like(x)
+        gu = randn((rows, 2 * inter), gen, torch.bfloat16, dev)
+        act = torch.empty((rows, inter), dtype=torch.bfloat16, device=dev)
+        row_bytes = hidden * 2
+        ops_ = {
+            "rms_norm": (lambda i: lib.crane_hip_rms_norm(x.data_ptr(), w.data_ptr(), out.data_ptr(), rows, hidden,
+                                                           1e-6, 1, st), 2 * rows * row_bytes + row_bytes),
+            "add_rms_norm": (lambda i: lib.crane_hip_add_rms_norm(x.data_ptr(), h.data_ptr(), w.data_ptr(),
+                                                                   out.data_ptr(), rows, hidden, 1e-6, 1, st),
+                             4 * rows * row_bytes + row_bytes),
+            "silu_mul": (lambda i: lib.crane_hip_silu_mul(gu.data_ptr(), act.data_ptr(), rows, inter, 1, st),
+                         3 * rows * inter * 2),
+            "residual_add": (lambda i: lib.crane_hip_residual_add(x.data_ptr(), h.data_ptr(), rows * hidden, 1, st),
+                             3 * rows * row_bytes),
+        }
+        res[tag] = {}
+        for name, (fn, nbytes) in ops_.items():
+            def launch(i, fn=fn, name=name):
+                rc = fn(i)
+                if rc:
+                    raise RuntimeError(f"{name} failed: {rc}")
+            ms = timed(launch, args.steps, args.warmup, stream)
+            gbs = nbytes / (ms * 1e-3) / 1e9
+            res[tag][name] = dict(us=ms * 1e3, gbs=gbs, frac=gbs / HBM_PEAK_GBS, bytes=nbytes)
+            log(f"[layer {tag}] {name}: {ms * 1e3:.1f} us, {gbs:.0f} GB/s ({gbs / HBM_PEAK_GBS * 100:.1f}% of HBM)")
+        del x, h, out, gu, act
+        torch.cuda.empty_cache()
+    return res
+
+
 # ---------------------------------------------------------------- prefill
 
 def bench_prefill(args, dev, stream, lib):
@@ -432,7 +476,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--only", choices=["decode", "prefill", "append", "all"], default="all")
+    ap.add_argument("--only", choices=["decode", "prefill", "append", "layer", "all"], default="all")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run a plain elementwise kernel over 1 GiB (scales FETCH_SIZE/WRITE_SIZE counters)")
@@ -476,6 +520,7 @@ def main():
             c2 = bench_prefill_c2(args, dev, stream, lib)
     if args.only in ("append", "all"):
         app = bench_append(args, dev, stream, lib)
+    lay = bench_layer(args, dev, stream, lib) if args.only in ("layer", "all") else None
     cpu = {} if args.no_cpu_baseline else cpu_baseline(dec, pre)
 
     traffic = pmc_traffic()
@@ -532,6 +577,9 @@ def main():
             a = app["c4_prefill_append"]
             line.update({"value": round(a["gbs"], 2), "unit": "GB/s", "ms_per_step": round(a["us"] / 1e3, 5),
                          "config": {"workload": "fused QK-norm+RoPE+KV append, c4 prefill size"}})
+    if lay is not None:
+        line["layer_ops"] = {t: {k: {kk: (round(vv, 4) if isinstance(vv, float) else vv) for kk, vv in v.items()}
+                                 for k, v in d.items()} for t, d in lay.items()}
     if "decode" in cpu:
         line["cpu_baseline"] = cpu["decode"]
     print(json.dumps(line), flush=True)

@@ -1,6 +1,7 @@
 """ctypes binding of libcrane_hip.so, the C ABI declared in include/crane_hip.h
-(attention launchers, dense and paged), include/crane_kv.h (host-side KV-cache
-manager) and include/crane_pkv.h (paged KV-cache manager).
+(attention launchers, dense and paged), include/crane_layer.h (the decoder
+layer's row kernels), include/crane_kv.h (host-side KV-cache manager) and
+include/crane_pkv.h (paged KV-cache manager).
 
 The library is the only compute path: there is no CPU fallback.  Loading
 fails loudly when the built library is missing.
@@ -58,6 +59,11 @@ SIGNATURES = {
         [_vp, _vp, _vp, _i64, _i, _i32p, _i64, _i32p, _i64, _i, _i, _i, _i, _f, _vp, _sz, _vp, _i, _vp], _i),
     "crane_hip_attn_prefill_paged": (
         [_vp, _vp, _vp, _i64, _i, _i32p, _i64, _i32p, _i64, _i, _i, _i, _i, _i, _f, _i, _vp, _i, _vp], _i),
+    # include/crane_layer.h
+    "crane_hip_rms_norm": ([_vp, _vp, _vp, _i64, _i, _f, _i, _vp], _i),
+    "crane_hip_add_rms_norm": ([_vp, _vp, _vp, _vp, _i64, _i, _f, _i, _vp], _i),
+    "crane_hip_silu_mul": ([_vp, _vp, _i64, _i, _i, _vp], _i),
+    "crane_hip_residual_add": ([_vp, _vp, _i64, _i, _vp], _i),
     # include/crane_pkv.h
     "crane_pkv_create": ([_i, _i, _i, _i, _i64, _i, _i, _vpp], _i),
     "crane_pkv_destroy": ([_vp], None),

@@ -84,6 +84,45 @@ __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_ex
 
 constexpr float kLog2e = 1.4426950408889634f;
 
+// ---- wave64 reductions with DPP (no LDS)
+template <int CTRL>
+__device__ __forceinline__ float dpp(float x) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, 0xf, 0xf, false));
+}
+
+// Sum over the 16 lanes of a DPP row; every lane gets the total.
+__device__ __forceinline__ float row16_sum(float x) {
+    x += dpp<0xB1>(x);   // quad_perm [1,0,3,2]
+    x += dpp<0x4E>(x);   // quad_perm [2,3,0,1]
+    x += dpp<0x124>(x);  // row_ror:4
+    x += dpp<0x128>(x);  // row_ror:8
+    return x;
+}
+
+
+// Whole-wave max / sum with DPP: reduce each 16-lane row, fold the rows with
+// row_bcast:15 / row_bcast:31 into lane 63, and broadcast it with readlane.
+template <int CTRL, int ROWS>
+__device__ __forceinline__ float dpp_rows(float x, float identity) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, identity),
+                                                                 __builtin_bit_cast(int, x), CTRL, ROWS, 0xf, false));
+}
+__device__ __forceinline__ float wave_max(float v) {
+    v = fmaxf(v, dpp<0xB1>(v));
+    v = fmaxf(v, dpp<0x4E>(v));
+    v = fmaxf(v, dpp<0x124>(v));
+    v = fmaxf(v, dpp<0x128>(v));
+    v = fmaxf(v, dpp_rows<0x142, 0xa>(v, -INFINITY));  // row_bcast:15 into rows 1, 3
+    v = fmaxf(v, dpp_rows<0x143, 0xc>(v, -INFINITY));  // row_bcast:31 into rows 2, 3
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
+}
+__device__ __forceinline__ float wave_sum(float v) {
+    v = row16_sum(v);
+    v += dpp_rows<0x142, 0xa>(v, 0.f);
+    v += dpp_rows<0x143, 0xc>(v, 0.f);
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
+}
+
 // Where row j of (sequence b, kv head kvh) of the K or V cache lives.
 // offset() is the element offset of the row inside its buffer, or -1 when the
 // row is past the sequence's capacity or its page id is outside the pool

@@ -331,3 +331,74 @@ def attention_prefill_paged(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch
         _stream(dev))
     check(rc, "attention_prefill_paged")
     return out
+
+
+# ------------------------------------------------------- decoder-layer rows
+# The row kernels either side of the attention block (include/crane_layer.h):
+# RmsNorm, residual add + RmsNorm, SiLU(gate) * up, residual add
+# (qwen3/modeling.rs:655-673, crane-core/src/fused_ops).
+
+def _rows_of(t: torch.Tensor, name: str):
+    _contig(t, name)
+    if t.dim() < 1:
+        raise CraneHipError(_lib.E_INVALID, f"{name} must have a last dimension")
+    cols = t.shape[-1]
+    return t.numel() // max(cols, 1), cols
+
+
+def rms_norm(x: torch.Tensor, weight: Optional[torch.Tensor] = None, eps: float = 1e-6) -> torch.Tensor:
+    """candle_nn::RmsNorm::forward over the last dimension of a contiguous x."""
+    dev = _dev(x, weight)
+    rows, cols = _rows_of(x, "x")
+    dt = _dtype_code(x)
+    if weight is not None and (weight.dtype != x.dtype or weight.numel() != cols or not weight.is_contiguous()):
+        raise CraneHipError(_lib.E_INVALID, "weight must be a contiguous [cols] tensor of x's dtype")
+    out = torch.empty_like(x)
+    check(_lib.lib().crane_hip_rms_norm(x.data_ptr(), _ptr(weight), out.data_ptr(), rows, cols, eps, dt,
+                                        _stream(dev)), "rms_norm")
+    return out
+
+
+def add_rms_norm(residual: torch.Tensor, hidden: torch.Tensor, weight: Optional[torch.Tensor] = None,
+                 eps: float = 1e-6) -> torch.Tensor:
+    """residual += hidden (in place, rounded to the dtype), then RmsNorm of the
+    new residual (Crane's FusedAddRmsNorm::fwd).  Returns the normed rows."""
+    dev = _dev(residual, hidden, weight)
+    if residual.shape != hidden.shape or residual.dtype != hidden.dtype:
+        raise CraneHipError(_lib.E_INVALID, "residual and hidden must have the same shape and dtype")
+    rows, cols = _rows_of(residual, "residual")
+    _contig(hidden, "hidden")
+    dt = _dtype_code(residual)
+    if weight is not None and (weight.dtype != residual.dtype or weight.numel() != cols or
+                               not weight.is_contiguous()):
+        raise CraneHipError(_lib.E_INVALID, "weight must be a contiguous [cols] tensor of the rows' dtype")
+    out = torch.empty_like(residual)
+    check(_lib.lib().crane_hip_add_rms_norm(residual.data_ptr(), hidden.data_ptr(), _ptr(weight), out.data_ptr(),
+                                            rows, cols, eps, dt, _stream(dev)), "add_rms_norm")
+    return out
+
+
+def silu_mul(gate_up: torch.Tensor, intermediate_size: Optional[int] = None) -> torch.Tensor:
+    """Crane's fused_silu_mul: gate_up [..., 2*I] (gate || up) -> silu(gate) * up [..., I]."""
+    dev = _dev(gate_up)
+    rows, last = _rows_of(gate_up, "gate_up")
+    inter = intermediate_size if intermediate_size is not None else last // 2
+    if last != 2 * inter:
+        raise CraneHipError(_lib.E_INVALID, f"last dim {last} != 2*intermediate_size {2 * inter}")
+    dt = _dtype_code(gate_up)
+    out = torch.empty(gate_up.shape[:-1] + (inter,), dtype=gate_up.dtype, device=dev)
+    check(_lib.lib().crane_hip_silu_mul(gate_up.data_ptr(), out.data_ptr(), rows, inter, dt, _stream(dev)),
+          "silu_mul")
+    return out
+
+
+def residual_add(residual: torch.Tensor, hidden: torch.Tensor) -> torch.Tensor:
+    """residual += hidden in place (rounded to the dtype); returns residual."""
+    dev = _dev(residual, hidden)
+    if residual.shape != hidden.shape or residual.dtype != hidden.dtype:
+        raise CraneHipError(_lib.E_INVALID, "residual and hidden must have the same shape and dtype")
+    _contig(residual, "residual")
+    _contig(hidden, "hidden")
+    check(_lib.lib().crane_hip_residual_add(residual.data_ptr(), hidden.data_ptr(), residual.numel(),
+                                            _dtype_code(residual), _stream(dev)), "residual_add")
+    return residual

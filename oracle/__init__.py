@@ -53,6 +53,8 @@ def lib():
                                             ctypes.c_int, _fp, _fp]
         L.orc_rms_norm.argtypes = [_fp, _fp, ctypes.c_size_t, ctypes.c_int, _fp,
                                    ctypes.c_float, ctypes.c_int, ctypes.c_int]
+        L.orc_silu_mul.argtypes = [_fp, _fp, ctypes.c_size_t, ctypes.c_int, ctypes.c_int, ctypes.c_int]
+        L.orc_residual_add.argtypes = [_fp, _fp, ctypes.c_size_t, ctypes.c_int]
         L.orc_rope.argtypes = [_fp, _fp, ctypes.c_size_t, ctypes.c_int, _fp, _fp, _ip,
                                ctypes.c_int]
         L.orc_qk_norm_rope_append.argtypes = [
@@ -128,6 +130,31 @@ def rms_norm(x: np.ndarray, w=None, eps: float = 1e-6, contiguous: bool = True, 
     wp = _f(np.ascontiguousarray(w, dtype=np.float32)) if w is not None else None
     lib().orc_rms_norm(_f(x), _f(y), x.size // d, d, wp, eps, int(contiguous), _dt(dtype))
     return y
+
+
+def silu_mul(gate_up: np.ndarray, f64: bool = False, dtype="f32"):
+    """Crane's fused SiLU(gate) * up over gate_up [..., 2*inter] (gate || up):
+    the f32 formula of its CUDA kernel, or (f64=True) its f64 cpu_fwd."""
+    gu = np.ascontiguousarray(gate_up, dtype=np.float32)
+    inter = gu.shape[-1] // 2
+    out = np.empty(gu.shape[:-1] + (inter,), dtype=np.float32)
+    lib().orc_silu_mul(_f(gu), _f(out), gu.size // (2 * inter), inter, int(f64), _dt(dtype))
+    return out
+
+
+def residual_add(residual: np.ndarray, hidden: np.ndarray, dtype="f32"):
+    """candle's `residual + hidden` in T (a new array)."""
+    r = np.ascontiguousarray(residual, dtype=np.float32).copy()
+    h = np.ascontiguousarray(hidden, dtype=np.float32)
+    assert r.shape == h.shape
+    lib().orc_residual_add(_f(r), _f(h), r.size, _dt(dtype))
+    return r
+
+
+def add_rms_norm(residual, hidden, w=None, eps: float = 1e-6, dtype="f32"):
+    """The candle pair Crane's FusedAddRmsNorm runs: (new residual, RmsNorm of it)."""
+    r = residual_add(residual, hidden, dtype)
+    return r, rms_norm(r, w, eps, True, dtype)
 
 
 def rope(x: np.ndarray, cos: np.ndarray, sin: np.ndarray, pos: np.ndarray, dtype="f32"):

@@ -449,3 +449,42 @@ void orc_attn_prefill(const float* q, const float* k_cache, const float* v_cache
         free(o);
     }
 }
+
+/* ------------------------------------------------- layer row operations -- */
+
+/* f64 -> bf16 with one round-to-nearest-even, as half::bf16::from_f64 (no
+ * intermediate f32 rounding).  Finite inputs in f32 range. */
+static float bf16_from_double(double x) {
+    if (x == 0.0 || !isfinite(x)) return (float)x;
+    int e;
+    frexp(x, &e);                               /* |x| in [2^(e-1), 2^e) */
+    if (e - 1 < -126) e = -126 + 1;             /* bf16 subnormals share f32's exponent floor */
+    const double ulp = ldexp(1.0, e - 1 - 7);   /* 8 significant bits */
+    return (float)(rint(x / ulp) * ulp);        /* x / ulp is exact; rint rounds to even */
+}
+
+void orc_silu_mul(const float* gate_up, float* out, size_t rows, int inter, int f64, int dtype) {
+    for (size_t r = 0; r < rows; ++r) {
+        const float* g = gate_up + r * 2 * (size_t)inter;
+        const float* u = g + inter;
+        float* o = out + r * (size_t)inter;
+        for (int i = 0; i < inter; ++i) {
+            if (f64) {
+                /* FusedSiluMul::cpu_fwd (cuda_impl.rs:65-76): f64 silu and product,
+                 * one conversion to T. */
+                const double gd = g[i];
+                const double s = gd / (1.0 + exp(-gd));
+                o[i] = dtype == ORC_BF16 ? bf16_from_double(s * (double)u[i]) : (float)(s * (double)u[i]);
+            } else {
+                /* fused_silu_mul_{bf16,f32} (fused_ops.cu:104-126, 163-182):
+                 * f32 g / (1 + expf(-g)) * u, one conversion to T. */
+                const float s = g[i] / (1.0f + expf(-g[i]));
+                o[i] = rd(s * u[i], dtype);
+            }
+        }
+    }
+}
+
+void orc_residual_add(float* residual, const float* hidden, size_t n, int dtype) {
+    for (size_t i = 0; i < n; ++i) residual[i] = rd(residual[i] + hidden[i], dtype);
+}

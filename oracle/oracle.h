@@ -63,6 +63,13 @@ void orc_rope_tables_qwen2(int dim, double theta, int max_pos, int dtype, float*
  * ops::rms_norm path (true for a contiguous input) or the LayerNorm fallback. */
 void orc_rms_norm(const float* x, float* y, size_t rows, int d, const float* w, float eps,
                   int contiguous, int dtype);
+/* Layer rows.  Crane's fused SiLU(gate) * up over
+ * gate_up [rows, 2*inter] (gate || up): f64 = 0 is the f32 formula of its CUDA
+ * kernel, f64 = 1 its cpu_fwd (f64, one conversion to T). */
+void orc_silu_mul(const float* gate_up, float* out, size_t rows, int inter, int f64, int dtype);
+/* candle's `residual + hidden` in T, in place. */
+void orc_residual_add(float* residual, const float* hidden, size_t n, int dtype);
+
 /* A6: candle_nn::rotary_emb::rope on rows of length d, row r using table row pos[r]. */
 void orc_rope(const float* x, float* y, size_t rows, int d, const float* cos, const float* sin,
               const int32_t* pos, int dtype);
