@@ -292,6 +292,43 @@ def bench_layer(args, dev, stream, lib):
     return res
 
 
+def bench_gemm(args, dev, stream, lib):
+    """The projections around attention (include/crane_gemm.h, hipBLASLt):
+    Qwen2.5-7B qkv_proj (with bias) and o_proj at config 4's 8 x 4096 rows, and
+    Qwen3-8B qkv_proj at config 3's 32 decode rows."""
+    import ctypes
+    import torch
+    h = ctypes.c_void_p()
+    if lib.crane_gemm_create(0, ctypes.byref(h)):
+        raise RuntimeError("crane_gemm_create failed")
+    st = stream.cuda_stream
+    res = {}
+    for tag, M, N, K, bias in (("c4_qkv_proj", 8 * 4096, 4608, 3584, True), ("c4_o_proj", 8 * 4096, 3584, 3584, False),
+                               ("c3_qkv_proj", 32, 6144, 4096, False)):
+        gen = torch.Generator(device=dev).manual_seed(SEED0 + 9)
+        x = randn((M, K), gen, torch.bfloat16, dev)
+        w = randn((N, K), gen, torch.bfloat16, dev, 1.0 / math.sqrt(K))
+        b = randn((N,), gen, torch.bfloat16, dev) if bias else None
+        y = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+
+        def launch(i):
+            rc = lib.crane_gemm_linear(h, x.data_ptr(), w.data_ptr(), b.data_ptr() if b is not None else None,
+                                       y.data_ptr(), M, N, K, 1, st)
+            if rc:
+                raise RuntimeError(f"crane_gemm_linear failed: {rc}")
+        ms = timed(launch, args.steps, args.warmup, stream)
+        flops = 2.0 * M * N * K
+        tf = flops / (ms * 1e-3) / 1e12
+        nbytes = (M * K + N * K + M * N) * 2
+        res[tag] = dict(us=ms * 1e3, tflops=tf, frac=tf / BF16_PEAK_TFLOPS, gbs=nbytes / (ms * 1e-3) / 1e9)
+        log(f"[gemm {tag}] M={M} N={N} K={K}: {ms * 1e3:.1f} us, {tf:.1f} TFLOP/s ({tf / BF16_PEAK_TFLOPS * 100:.1f}% "
+            f"of bf16 peak), {res[tag]['gbs']:.0f} GB/s")
+        del x, w, b, y
+    lib.crane_gemm_destroy(h)
+    torch.cuda.empty_cache()
+    return res
+
+
 # ---------------------------------------------------------------- prefill
 
 def bench_prefill(args, dev, stream, lib):
@@ -476,7 +513,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--only", choices=["decode", "prefill", "append", "layer", "all"], default="all")
+    ap.add_argument("--only", choices=["decode", "prefill", "append", "layer", "gemm", "all"], default="all")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run a plain elementwise kernel over 1 GiB (scales FETCH_SIZE/WRITE_SIZE counters)")
@@ -521,6 +558,7 @@ def main():
     if args.only in ("append", "all"):
         app = bench_append(args, dev, stream, lib)
     lay = bench_layer(args, dev, stream, lib) if args.only in ("layer", "all") else None
+    gem = bench_gemm(args, dev, stream, lib) if args.only in ("gemm", "all") else None
     cpu = {} if args.no_cpu_baseline else cpu_baseline(dec, pre)
 
     traffic = pmc_traffic()
@@ -580,6 +618,8 @@ def main():
     if lay is not None:
         line["layer_ops"] = {t: {k: {kk: (round(vv, 4) if isinstance(vv, float) else vv) for kk, vv in v.items()}
                                  for k, v in d.items()} for t, d in lay.items()}
+    if gem is not None:
+        line["gemm"] = {t: {k: round(v, 4) for k, v in d.items()} for t, d in gem.items()}
     if "decode" in cpu:
         line["cpu_baseline"] = cpu["decode"]
     print(json.dumps(line), flush=True)

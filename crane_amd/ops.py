@@ -11,6 +11,7 @@ fallback.
 """
 from __future__ import annotations
 
+import ctypes
 import math
 from typing import Optional
 
@@ -402,3 +403,56 @@ def residual_add(residual: torch.Tensor, hidden: torch.Tensor) -> torch.Tensor:
     check(_lib.lib().crane_hip_residual_add(residual.data_ptr(), hidden.data_ptr(), residual.numel(),
                                             _dtype_code(residual), _stream(dev)), "residual_add")
     return residual
+
+
+# ------------------------------------------------------------- projections
+# candle Linear (y = x W^T + b) on hipBLASLt (include/crane_gemm.h): the merged
+# qkv_proj whose output rows feed qk_norm_rope_append, and o_proj.
+
+class _GemmContext:
+    """One crane_gemm (hipBLASLt handle, workspace, per-shape plans) per device."""
+
+    def __init__(self, device: torch.device):
+        h = ctypes.c_void_p()
+        with torch.cuda.device(device):
+            check(_lib.lib().crane_gemm_create(0, ctypes.byref(h)), "crane_gemm_create")
+        self._h = h
+        self._destroy = _lib.lib().crane_gemm_destroy  # bound now: usable during interpreter shutdown
+
+    def __del__(self):
+        if getattr(self, "_h", None):
+            self._destroy(self._h)
+            self._h = None
+
+
+_GEMMS: dict = {}
+
+
+def _gemm(device: torch.device) -> _GemmContext:
+    ctx = _GEMMS.get(device)
+    if ctx is None:
+        ctx = _GEMMS[device] = _GemmContext(device)
+    return ctx
+
+
+def linear(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """candle Linear::forward: x [..., K] with weight [N, K] (and bias [N]) ->
+    [..., N]; f32 accumulation, the bias added in the GEMM epilogue."""
+    dev = _dev(x, weight, bias)
+    K = x.shape[-1]
+    if weight.dim() != 2 or weight.shape[1] != K:
+        raise CraneHipError(_lib.E_INVALID, f"weight must be [N, {K}]")
+    N = weight.shape[0]
+    for t, name in ((x, "x"), (weight, "weight"), (bias, "bias")):
+        if t is not None:
+            _contig(t, name)
+            if t.dtype != x.dtype:
+                raise CraneHipError(_lib.E_DTYPE, f"{name} dtype {t.dtype} != {x.dtype}")
+    if bias is not None and bias.numel() != N:
+        raise CraneHipError(_lib.E_INVALID, f"bias must have {N} elements")
+    dt = _dtype_code(x)
+    M = x.numel() // K
+    y = torch.empty(x.shape[:-1] + (N,), dtype=x.dtype, device=dev)
+    check(_lib.lib().crane_gemm_linear(_gemm(dev)._h, x.data_ptr(), weight.data_ptr(), _ptr(bias), y.data_ptr(),
+                                       M, N, K, dt, _stream(dev)), "linear")
+    return y

@@ -1,0 +1,47 @@
+/*
+ * crane_gemm.h -- C ABI of the projections around the attention block: the
+ * merged QKV projection that feeds crane_hip_qknorm_rope_append and o_proj
+ * that consumes the attention output (gfx950, hipBLASLt).
+ *
+ * Crane's projections are candle Linear layers (qwen3/modeling.rs:207-223,
+ * 382-387 qkv_proj; :466 and :502 o_proj; the QKV bias of Qwen2.5,
+ * qwen25/qwen2.rs:136-138): y = x W^T (+ b) with W stored [N, K] (out
+ * features x in features, row-major) and x [M, K] row-major.  The merged qkv
+ * output [M, (Hq + 2 Hkv) D] is exactly the `qkv` rows of the fused append,
+ * and the attention output [B, S, Hq D] is exactly o_proj's x.
+ *
+ * These are plain library GEMMs: hipBLASLt with f32 accumulation, the bias
+ * added in the epilogue (one rounding of acc + b, where candle rounds the
+ * product and then the sum).  A crane_gemm context holds the hipBLASLt handle,
+ * a workspace allocated at creation and the algorithm chosen for each shape
+ * (the heuristic query runs once per shape).  Conventions otherwise as in
+ * crane_hip.h; crane_gemm_linear does not allocate or synchronise.  One
+ * context must not be used from two threads at once; it belongs to the device
+ * that was current at creation.
+ */
+#ifndef CRANE_GEMM_H
+#define CRANE_GEMM_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct crane_gemm crane_gemm;
+
+/* A context with `workspace_bytes` of GEMM workspace (0 for the default, 32 MiB). */
+int crane_gemm_create(size_t workspace_bytes, crane_gemm** out);
+void crane_gemm_destroy(crane_gemm* g);
+
+/* y[M, N] = x[M, K] W[N, K]^T (+ bias[N]) in `dtype` (CRANE_HIP_F32 or
+ * CRANE_HIP_BF16), f32 accumulation; bias may be NULL.  Pointers are 16-byte
+ * aligned; M, N, K > 0 (M == 0 does nothing). */
+int crane_gemm_linear(crane_gemm* g, const void* x, const void* w, const void* bias, void* y, int64_t M, int64_t N,
+                      int64_t K, int dtype, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* CRANE_GEMM_H */

@@ -55,6 +55,8 @@ def lib():
                                    ctypes.c_float, ctypes.c_int, ctypes.c_int]
         L.orc_silu_mul.argtypes = [_fp, _fp, ctypes.c_size_t, ctypes.c_int, ctypes.c_int, ctypes.c_int]
         L.orc_residual_add.argtypes = [_fp, _fp, ctypes.c_size_t, ctypes.c_int]
+        L.orc_linear.argtypes = [_fp, _fp, _fp, _fp, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                 ctypes.c_int]
         L.orc_rope.argtypes = [_fp, _fp, ctypes.c_size_t, ctypes.c_int, _fp, _fp, _ip,
                                ctypes.c_int]
         L.orc_qk_norm_rope_append.argtypes = [
@@ -149,6 +151,20 @@ def residual_add(residual: np.ndarray, hidden: np.ndarray, dtype="f32"):
     assert r.shape == h.shape
     lib().orc_residual_add(_f(r), _f(h), r.size, _dt(dtype))
     return r
+
+
+def linear(x: np.ndarray, w: np.ndarray, bias=None, dtype="f32", fused: bool = False):
+    """candle Linear: x [..., K] times w [N, K]^T (+ bias [N]) -> [..., N];
+    fused=True rounds product + bias once (a GEMM epilogue)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    N, K = w.shape
+    assert x.shape[-1] == K
+    M = x.size // K
+    y = np.empty(x.shape[:-1] + (N,), dtype=np.float32)
+    bp = _f(np.ascontiguousarray(bias, dtype=np.float32)) if bias is not None else None
+    lib().orc_linear(_f(x), _f(w), bp, _f(y), M, N, K, int(fused), _dt(dtype))
+    return y
 
 
 def add_rms_norm(residual, hidden, w=None, eps: float = 1e-6, dtype="f32"):

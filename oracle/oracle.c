@@ -488,3 +488,29 @@ void orc_silu_mul(const float* gate_up, float* out, size_t rows, int inter, int 
 void orc_residual_add(float* residual, const float* hidden, size_t n, int dtype) {
     for (size_t i = 0; i < n; ++i) residual[i] = rd(residual[i] + hidden[i], dtype);
 }
+
+/* candle Linear::forward (x.matmul(w.t()) then broadcast_add(bias), the merged
+ * qkv_proj of qwen3/modeling.rs:382-387 and o_proj): the product accumulated
+ * in f64 and converted to T once, then the bias added in T.  fused = 1 rounds
+ * product + bias once instead (a GEMM epilogue's semantics). */
+void orc_linear(const float* x, const float* w, const float* bias, float* y, int M, int N, int K, int fused,
+                int dtype) {
+#pragma omp parallel for schedule(static)
+    for (int m = 0; m < M; ++m) {
+        const float* xr = x + (size_t)m * K;
+        for (int n = 0; n < N; ++n) {
+            const float* wr = w + (size_t)n * K;
+            double acc = 0.0;
+            for (int k = 0; k < K; ++k) acc += (double)xr[k] * (double)wr[k];
+            float p;
+            if (bias && fused) {
+                acc += (double)bias[n];
+                p = dtype == ORC_BF16 ? bf16_from_double(acc) : (float)acc;
+            } else {
+                p = dtype == ORC_BF16 ? bf16_from_double(acc) : (float)acc;
+                if (bias) p = rd(p + bias[n], dtype);
+            }
+            y[(size_t)m * N + n] = p;
+        }
+    }
+}

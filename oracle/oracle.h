@@ -69,6 +69,11 @@ void orc_rms_norm(const float* x, float* y, size_t rows, int d, const float* w, 
 void orc_silu_mul(const float* gate_up, float* out, size_t rows, int inter, int f64, int dtype);
 /* candle's `residual + hidden` in T, in place. */
 void orc_residual_add(float* residual, const float* hidden, size_t n, int dtype);
+/* candle Linear: y[M,N] = T(T(x[M,K] w[N,K]^T) + bias[N]) (bias may be NULL);
+ * the product is accumulated in f64 and converted to T once.  fused = 1:
+ * T(x w^T + bias) with one conversion (a GEMM epilogue's rounding). */
+void orc_linear(const float* x, const float* w, const float* bias, float* y, int M, int N, int K, int fused,
+                int dtype);
 
 /* A6: candle_nn::rotary_emb::rope on rows of length d, row r using table row pos[r]. */
 void orc_rope(const float* x, float* y, size_t rows, int d, const float* cos, const float* sin,

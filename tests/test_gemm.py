@@ -1,0 +1,130 @@
+"""The projections around the attention block (include/crane_gemm.h): candle
+Linear y = x W^T + b on hipBLASLt -- Crane's merged qkv_proj, whose rows feed
+the fused append (qwen3/modeling.rs:382-387; with the Qwen2.5 bias,
+qwen25/qwen2.rs:136-138), and o_proj (:466, :502).
+
+The oracle's linear is pinned to numpy float64 matmul (a transposed weight
+fails); the GPU is held to the oracle within the rounding bound of its two
+differences (f32 accumulation in another order, and one rounding of product
++ bias where candle rounds twice) and the mean-relative bar, with weights
+scaled like trained ones (std 1/sqrt(K)) so outputs are O(1)."""
+import math
+
+import numpy as np
+import pytest
+
+import cases
+from tolerance import assert_close, assert_ulp_close, bf16_ulp
+
+
+def assert_linear_close(got, x, w, bias, dtype, orc, what):
+    """Two references.  Against the oracle with the GPU's rounding (product +
+    bias rounded once) every element lies within the f32 accumulation bound,
+    K * 2^-24 * sum|x||w| (any summation order) plus one ulp, and at least 99%
+    of them are bit-identical.  Against candle's (product rounded, then the
+    sum) the two roundings differ by at most half an ulp at |p| plus an ulp at
+    |y|: elements within 1.5 ulp of max(|y|, |p|, |b|) plus the accumulation
+    bound, and the mean-relative bar.  f32: the f32 bar."""
+    ref = orc.linear(x, w, bias, dtype)
+    if dtype == "f32":
+        return assert_close(got, ref, dtype, what)
+    K = x.shape[-1]
+    acc = (K * 2.0 ** -24) * (np.abs(x.astype(np.float64)) @ np.abs(w.astype(np.float64)).T)
+    fused = orc.linear(x, w, bias, dtype, fused=True)
+    d = np.abs(got.astype(np.float64) - fused)
+    assert np.all(d <= acc + bf16_ulp(fused)), f"{what}: beyond the accumulation bound"
+    exact = float(np.mean(got == fused))
+    assert exact >= 0.99, f"{what}: only {exact:.4f} bit-identical to the fused-rounding oracle"
+    b = np.zeros(ref.shape[-1], np.float32) if bias is None else bias
+    scale = np.maximum(np.maximum(np.abs(ref), np.abs(ref - b)), np.abs(b))
+    d2 = np.abs(got.astype(np.float64) - ref)
+    assert np.all(d2 <= 1.5 * bf16_ulp(scale) + acc), f"{what}: beyond the candle rounding bound"
+    from tolerance import errors, BF16_MEAN_REL
+    assert errors(got, ref)[1] <= BF16_MEAN_REL, what
+
+
+def _case(seed, M, N, K, dtype, bias=True):
+    r = cases.rng(seed)
+    x = cases.cast(cases.normal(r, (M, K)), dtype)
+    w = cases.cast(cases.normal(r, (N, K), 1.0 / math.sqrt(K)), dtype)
+    b = cases.cast(cases.normal(r, (N,), 0.5), dtype) if bias else None
+    return x, w, b
+
+
+# ------------------------------------------------------------------ CPU
+
+def test_linear_oracle_vs_numpy_float64(orc):
+    x, w, b = _case(1, 37, 96, 640, "bf16")
+    exact = x.astype(np.float64) @ w.astype(np.float64).T
+    y32 = orc.linear(x, w, None, "f32")
+    assert np.max(np.abs(y32 - exact) / np.maximum(np.abs(exact), 1e-6)) < 1.5e-7
+    yb = orc.linear(x, w, None, "bf16")
+    assert np.all(np.abs(yb - exact) <= 0.5 * bf16_ulp(exact) * (1 + 1e-9))   # one rounding
+    ybb = orc.linear(x, w, b, "bf16")
+    np.testing.assert_array_equal(ybb, cases.bf16(yb + b[None, :]))          # then the bias in T
+    wrong = orc.linear(x, np.ascontiguousarray(w[:, ::-1]), None, "f32")      # a planted mistake
+    assert np.max(np.abs(wrong - exact)) > 0.5
+    fb = orc.linear(x, w, b, "bf16", fused=True)                               # epilogue rounding
+    assert np.all(np.abs(fb - (exact + b)) <= 0.5 * bf16_ulp(exact + b) * (1 + 1e-9))
+
+
+def test_gemm_null_context():
+    from crane_amd import _lib
+    assert _lib.lib().crane_gemm_linear(None, 16, 16, None, 16, 4, 4, 4, 1, None) == _lib.E_INVALID
+
+
+# ------------------------------------------------------------------ GPU
+
+def _t(x, dtype, dev):
+    import torch
+    t = torch.from_numpy(np.ascontiguousarray(x))
+    return (t.to(torch.bfloat16) if dtype == "bf16" else t).to(dev)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype", ["bf16", "f32"])
+@pytest.mark.parametrize("M,N,K,bias", [
+    (64, 4608, 3584, True),    # Qwen2.5-7B qkv_proj (28 q + 2 x 4 kv heads), with bias
+    (32, 6144, 4096, False),   # Qwen3-8B qkv_proj at the c3 decode batch
+    (300, 3584, 3584, False),  # Qwen2.5-7B o_proj
+    (5, 136, 72, True),        # odd small shape
+])
+def test_linear_parity(gpu, orc, dtype, M, N, K, bias):
+    from crane_amd import ops
+    print(f"linear {dtype} M={M} N={N} K={K} bias={bias}", flush=True)
+    x, w, b = _case(500 + N, M, N, K, dtype, bias)
+    got = ops.linear(_t(x, dtype, gpu), _t(w, dtype, gpu), _t(b, dtype, gpu) if bias else None)
+    assert_linear_close(got.float().cpu().numpy(), x, w, b, dtype, orc, f"linear {M}x{N}x{K}")
+    # twice: the cached plan gives the same bits
+    got2 = ops.linear(_t(x, dtype, gpu), _t(w, dtype, gpu), _t(b, dtype, gpu) if bias else None)
+    assert bool((got == got2).all())
+
+
+@pytest.mark.gpu
+def test_qkv_proj_feeds_the_append(gpu, orc):
+    """Hidden states -> qkv_proj (bias) -> fused QK-norm/RoPE append, against
+    the oracle's Linear followed by its append."""
+    import torch
+    from crane_amd import ops
+    B, S, H, Hq, Hkv, D = 2, 33, 512, 8, 2, 128
+    W = (Hq + 2 * Hkv) * D
+    x, w, b = _case(600, B * S, W, H, "bf16")
+    qkv = ops.linear(_t(x, "bf16", gpu), _t(w, "bf16", gpu), _t(b, "bf16", gpu)).reshape(B, S, W)
+    assert_linear_close(qkv.float().cpu().numpy().reshape(B * S, W), x, w, b, "bf16", orc, "qkv_proj")
+    cos, sin = orc.rope_tables(D, 1e6, 64)
+    cos, sin = orc.round_bf16(cos), orc.round_bf16(sin)
+    kc = torch.zeros((B, Hkv, 64, D), dtype=torch.bfloat16, device=gpu)
+    vc = torch.zeros_like(kc)
+    zero = torch.zeros(B, dtype=torch.int32, device=gpu)
+    q = ops.qk_norm_rope_append(qkv, _t(cos, "bf16", gpu), _t(sin, "bf16", gpu), zero, kc, vc, zero, S, Hq, Hkv,
+                                order="rope_only")
+    kref = np.zeros((B, Hkv, 64, D), np.float32)
+    vref = np.zeros_like(kref)
+    # the append is applied to the GPU's own qkv rows: this checks the hand-off
+    # (layout and row stride), the append's parity is tested on its own
+    qkv_np = qkv.float().cpu().numpy()
+    q_ref = orc.qk_norm_rope_append(qkv_np, Hq, Hkv, cos, sin, np.zeros(B, np.int32), kref, vref,
+                                    np.zeros(B, np.int32), order=orc.ROPE_ONLY, dtype="bf16")
+    assert_ulp_close(q.float().cpu().numpy(), q_ref, "bf16", "q after the append", min_exact=0.999)
+    assert_ulp_close(kc.float().cpu().numpy(), kref, "bf16", "k cache after the append", min_exact=0.999)
+    np.testing.assert_array_equal(vc.float().cpu().numpy(), vref)
