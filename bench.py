@@ -329,6 +329,30 @@ def bench_gemm(args, dev, stream, lib):
     return res
 
 
+def bench_sampling(args, dev, stream, lib):
+    """Token selection over Qwen vocabulary logits (151936): argmax on bf16
+    (greedy) and top-64 on f32, one row and a c3 batch of 32 rows."""
+    import torch
+    res = {}
+    st = stream.cuda_stream
+    n = 151936
+    for rows in (1, 32):
+        gen = torch.Generator(device=dev).manual_seed(SEED0 + 11)
+        xb = randn((rows, n), gen, torch.bfloat16, dev, 4.0)
+        xf = randn((rows, n), gen, torch.float32, dev, 4.0)
+        out = torch.empty((rows, 64), dtype=torch.int32, device=dev)
+        for name, fn in (("argmax_bf16", lambda i: lib.crane_hip_argmax(xb.data_ptr(), rows, n, 1, out.data_ptr(), st)),
+                         ("topk64_f32", lambda i: lib.crane_hip_topk(xf.data_ptr(), rows, n, 64, out.data_ptr(), st))):
+            def launch(i, fn=fn, name=name):
+                rc = fn(i)
+                if rc:
+                    raise RuntimeError(f"{name} failed: {rc}")
+            ms = timed(launch, args.steps, args.warmup, stream)
+            res[f"{name}_rows{rows}"] = dict(us=ms * 1e3)
+            log(f"[sampling] {name} {rows} x {n}: {ms * 1e3:.1f} us")
+    return res
+
+
 # ---------------------------------------------------------------- prefill
 
 def bench_prefill(args, dev, stream, lib):
@@ -513,7 +537,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--only", choices=["decode", "prefill", "append", "layer", "gemm", "all"], default="all")
+    ap.add_argument("--only", choices=["decode", "prefill", "append", "layer", "gemm", "sampling", "all"], default="all")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run a plain elementwise kernel over 1 GiB (scales FETCH_SIZE/WRITE_SIZE counters)")
@@ -559,6 +583,7 @@ def main():
         app = bench_append(args, dev, stream, lib)
     lay = bench_layer(args, dev, stream, lib) if args.only in ("layer", "all") else None
     gem = bench_gemm(args, dev, stream, lib) if args.only in ("gemm", "all") else None
+    smp = bench_sampling(args, dev, stream, lib) if args.only in ("sampling", "all") else None
     cpu = {} if args.no_cpu_baseline else cpu_baseline(dec, pre)
 
     traffic = pmc_traffic()
@@ -620,6 +645,8 @@ def main():
                                  for k, v in d.items()} for t, d in lay.items()}
     if gem is not None:
         line["gemm"] = {t: {k: round(v, 4) for k, v in d.items()} for t, d in gem.items()}
+    if smp is not None:
+        line["sampling"] = {t: {k: round(v, 2) for k, v in d.items()} for t, d in smp.items()}
     if "decode" in cpu:
         line["cpu_baseline"] = cpu["decode"]
     print(json.dumps(line), flush=True)

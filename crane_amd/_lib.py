@@ -1,6 +1,7 @@
 """ctypes binding of libcrane_hip.so, the C ABI declared in include/crane_hip.h
 (attention launchers, dense and paged), include/crane_layer.h (the decoder
-layer's row kernels), include/crane_gemm.h (the QKV / o_proj projections), include/crane_kv.h (host-side KV-cache manager) and
+layer's row kernels), include/crane_gemm.h (the QKV / o_proj projections), include/crane_sampling.h
+(argmax, top-k), include/crane_kv.h (host-side KV-cache manager) and
 include/crane_pkv.h (paged KV-cache manager).
 
 The library is the only compute path: there is no CPU fallback.  Loading
@@ -64,6 +65,9 @@ SIGNATURES = {
     "crane_hip_add_rms_norm": ([_vp, _vp, _vp, _vp, _i64, _i, _f, _i, _vp], _i),
     "crane_hip_silu_mul": ([_vp, _vp, _i64, _i, _i, _vp], _i),
     "crane_hip_residual_add": ([_vp, _vp, _i64, _i, _vp], _i),
+    # include/crane_sampling.h
+    "crane_hip_argmax": ([_vp, _i64, _i64, _i, _vp, _vp], _i),
+    "crane_hip_topk": ([_vp, _i64, _i64, _i, _vp, _vp], _i),
     # include/crane_gemm.h
     "crane_gemm_create": ([_sz, _vpp], _i),
     "crane_gemm_destroy": ([_vp], None),

@@ -456,3 +456,34 @@ def linear(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor] =
     check(_lib.lib().crane_gemm_linear(_gemm(dev)._h, x.data_ptr(), weight.data_ptr(), _ptr(bias), y.data_ptr(),
                                        M, N, K, dt, _stream(dev)), "linear")
     return y
+
+
+# ---------------------------------------------------------------- sampling
+# Token selection on the logits (include/crane_sampling.h): Crane's gpu_argmax
+# (greedy) and topk_indices (top-k / top-p candidates), batched over rows.
+
+def argmax(logits: torch.Tensor) -> torch.Tensor:
+    """Index of the largest value of every row of logits [..., n] (first one
+    on ties); int32 [...]."""
+    dev = _dev(logits)
+    _contig(logits, "logits")
+    n = logits.shape[-1]
+    rows = logits.numel() // max(n, 1)
+    out = torch.empty(logits.shape[:-1], dtype=torch.int32, device=dev)
+    check(_lib.lib().crane_hip_argmax(logits.data_ptr(), rows, n, _dtype_code(logits), out.data_ptr(), _stream(dev)),
+          "argmax")
+    return out
+
+
+def topk_indices(x: torch.Tensor, k: int) -> torch.Tensor:
+    """Indices of the k largest values of every row of x [..., n] (f32),
+    largest first, ties by lower index; int32 [..., k]."""
+    dev = _dev(x)
+    _contig(x, "x")
+    if x.dtype != torch.float32:
+        raise CraneHipError(_lib.E_DTYPE, "topk_indices takes f32 logits")
+    n = x.shape[-1]
+    rows = x.numel() // max(n, 1)
+    out = torch.empty(x.shape[:-1] + (k,), dtype=torch.int32, device=dev)
+    check(_lib.lib().crane_hip_topk(x.data_ptr(), rows, n, k, out.data_ptr(), _stream(dev)), "topk_indices")
+    return out

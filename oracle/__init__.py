@@ -55,6 +55,9 @@ def lib():
                                    ctypes.c_float, ctypes.c_int, ctypes.c_int]
         L.orc_silu_mul.argtypes = [_fp, _fp, ctypes.c_size_t, ctypes.c_int, ctypes.c_int, ctypes.c_int]
         L.orc_residual_add.argtypes = [_fp, _fp, ctypes.c_size_t, ctypes.c_int]
+        _up = ctypes.POINTER(ctypes.c_uint32)
+        L.orc_argmax.argtypes = [_fp, ctypes.c_size_t, ctypes.c_size_t, _up]
+        L.orc_topk.argtypes = [_fp, ctypes.c_size_t, ctypes.c_size_t, ctypes.c_int, _up]
         L.orc_linear.argtypes = [_fp, _fp, _fp, _fp, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
                                  ctypes.c_int]
         L.orc_rope.argtypes = [_fp, _fp, ctypes.c_size_t, ctypes.c_int, _fp, _fp, _ip,
@@ -165,6 +168,25 @@ def linear(x: np.ndarray, w: np.ndarray, bias=None, dtype="f32", fused: bool = F
     bp = _f(np.ascontiguousarray(bias, dtype=np.float32)) if bias is not None else None
     lib().orc_linear(_f(x), _f(w), bp, _f(y), M, N, K, int(fused), _dt(dtype))
     return y
+
+
+def argmax(x: np.ndarray) -> np.ndarray:
+    """First maximum of every row of x [..., n] (NaN lowest, -0 == +0)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    n = x.shape[-1]
+    out = np.empty(x.size // n, dtype=np.uint32)
+    lib().orc_argmax(_f(x), out.size, n, out.ctypes.data_as(ctypes.POINTER(ctypes.c_uint32)))
+    return out.reshape(x.shape[:-1])
+
+
+def topk(x: np.ndarray, k: int) -> np.ndarray:
+    """Indices of the k largest of every row (value descending, index ascending)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    n = x.shape[-1]
+    rows = x.size // n
+    out = np.empty((rows, k), dtype=np.uint32)
+    lib().orc_topk(_f(x), rows, n, k, out.ctypes.data_as(ctypes.POINTER(ctypes.c_uint32)))
+    return out.reshape(x.shape[:-1] + (k,))
 
 
 def add_rms_norm(residual, hidden, w=None, eps: float = 1e-6, dtype="f32"):

@@ -514,3 +514,58 @@ void orc_linear(const float* x, const float* w, const float* bias, float* y, int
         }
     }
 }
+
+/* --------------------------------------------------------------- sampling -- */
+
+/* Order of crane_sampling.h: value descending, then index ascending; NaN
+ * below every number, -0 equal to +0. */
+static inline uint32_t order_key(float v) {
+    uint32_t u;
+    memcpy(&u, &v, 4);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return 0u;
+    if (u == 0x80000000u) u = 0u;
+    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+static int before(float a, uint32_t ia, float b, uint32_t ib) {
+    const uint32_t ka = order_key(a), kb = order_key(b);
+    return ka != kb ? ka > kb : ia < ib;
+}
+
+/* gpu_argmax / candle argmax (first maximum) per row. */
+void orc_argmax(const float* x, size_t rows, size_t n, uint32_t* out) {
+    for (size_t r = 0; r < rows; ++r) {
+        const float* xr = x + r * n;
+        uint32_t best = 0;
+        for (size_t i = 1; i < n; ++i)
+            if (before(xr[i], (uint32_t)i, xr[best], best)) best = (uint32_t)i;
+        out[r] = best;
+    }
+}
+
+/* topk_indices per row: the first k elements in that order (a full sort of
+ * (key, index) pairs, k <= 64). */
+typedef struct {
+    uint32_t key, idx;
+} orc_pair;
+
+static int pair_cmp(const void* a, const void* b) {
+    const orc_pair* p = (const orc_pair*)a;
+    const orc_pair* q = (const orc_pair*)b;
+    if (p->key != q->key) return p->key > q->key ? -1 : 1;
+    return p->idx < q->idx ? -1 : (p->idx > q->idx ? 1 : 0);
+}
+
+void orc_topk(const float* x, size_t rows, size_t n, int k, uint32_t* out) {
+    orc_pair* pairs = (orc_pair*)malloc(n * sizeof(orc_pair));
+    for (size_t r = 0; r < rows; ++r) {
+        const float* xr = x + r * n;
+        for (size_t i = 0; i < n; ++i) {
+            pairs[i].key = order_key(xr[i]);
+            pairs[i].idx = (uint32_t)i;
+        }
+        qsort(pairs, n, sizeof(orc_pair), pair_cmp);
+        for (int j = 0; j < k; ++j) out[r * k + j] = pairs[j].idx;
+    }
+    free(pairs);
+}

@@ -75,6 +75,11 @@ void orc_residual_add(float* residual, const float* hidden, size_t n, int dtype)
 void orc_linear(const float* x, const float* w, const float* bias, float* y, int M, int N, int K, int fused,
                 int dtype);
 
+/* Sampling (crane_sampling.h order: value descending, index ascending, NaN
+ * lowest, -0 == +0): the first maximum per row, and the first k per row. */
+void orc_argmax(const float* x, size_t rows, size_t n, uint32_t* out);
+void orc_topk(const float* x, size_t rows, size_t n, int k, uint32_t* out);
+
 /* A6: candle_nn::rotary_emb::rope on rows of length d, row r using table row pos[r]. */
 void orc_rope(const float* x, float* y, size_t rows, int d, const float* cos, const float* sin,
               const int32_t* pos, int dtype);
