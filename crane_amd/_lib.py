@@ -32,6 +32,8 @@ SIGNATURES = {
     "crane_hip_qknorm_rope_append": (
         [_vp, _i64, _vp, _vp, _f, _i, _vp, _vp, _i64, _i64, _i32p, _vp, _vp, _vp, _i64, _i32p, _i64,
          _i, _i, _i, _i, _i, _i, _vp], _i),
+    "crane_hip_qnorm_rope": (
+        [_vp, _i64, _vp, _f, _i, _vp, _vp, _i64, _i64, _i32p, _vp, _i, _i, _i, _i, _i, _vp], _i),
     "crane_hip_attn_decode_workspace": ([_i, _i, _i, _i, _i64, _i], _sz),
     "crane_hip_attn_decode": (
         [_vp, _vp, _vp, _i64, _i32p, _i64, _i, _i, _i, _i, _f, _vp, _sz, _vp, _i, _vp], _i),

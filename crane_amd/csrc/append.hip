@@ -186,6 +186,44 @@ extern "C" int crane_hip_qknorm_rope_append(const void* qkv, int64_t qkv_row_str
                               dtype, stream);
 }
 
+// The Hunyuan CLA layer (hunyuan_dense/modeling.rs:502-514) projects only q and
+// attends over the anchor layer's cache: the same kernel over Hq head rows per
+// token with no key or value heads, so no cache is addressed or written.
+extern "C" int crane_hip_qnorm_rope(const void* q, int64_t q_row_stride, const void* q_norm_w, float eps, int order,
+                                    const void* cos, const void* sin, int64_t cs_stride, int64_t table_rows,
+                                    const int32_t* positions, void* q_out, int B, int S, int Hq, int D, int dtype,
+                                    void* stream) {
+    if (dtype != CRANE_HIP_F32 && dtype != CRANE_HIP_BF16) return CRANE_HIP_E_DTYPE;
+    if (D != kHeadDim) return CRANE_HIP_E_HEAD_DIM;
+    if (B < 0 || S < 0 || Hq <= 0) return CRANE_HIP_E_INVALID;
+    if (order < CRANE_HIP_NORM_THEN_ROPE || order > CRANE_HIP_ROPE_ONLY) return CRANE_HIP_E_INVALID;
+    if (!(eps >= 0.0f)) return CRANE_HIP_E_INVALID;
+    if (B == 0 || S == 0) return CRANE_HIP_OK;
+    if (!q || !cos || !sin || !positions || !q_out) return CRANE_HIP_E_INVALID;
+    if (q_row_stride < (int64_t)Hq * D || cs_stride < D / 2 || table_rows <= 0) return CRANE_HIP_E_INVALID;
+    if (q_row_stride % 4 != 0 || cs_stride % 4 != 0) return CRANE_HIP_E_ALIGN;
+    if (!aligned16(q) || !aligned16(cos) || !aligned16(sin) || !aligned16(q_out) || (q_norm_w && !aligned16(q_norm_w)))
+        return CRANE_HIP_E_ALIGN;
+    const int64_t n_items = (int64_t)B * S * Hq;
+    const int64_t blocks = (n_items + kItemsPerBlock - 1) / kItemsPerBlock;
+    if (blocks > 0x7fffffffLL) return CRANE_HIP_E_INVALID;
+    hipStream_t st = (hipStream_t)stream;
+    const DenseRows none{1};  // never consulted: every item is a q head
+    if (dtype == CRANE_HIP_F32) {
+        hipLaunchKernelGGL((qknorm_rope_append_kernel<float, DenseRows>), dim3((unsigned)blocks), dim3(256), 0, st,
+                           (const float*)q, q_row_stride, (const float*)q_norm_w, (const float*)nullptr, eps, order,
+                           (const float*)cos, (const float*)sin, cs_stride, table_rows, positions, (float*)q_out,
+                           (float*)nullptr, (float*)nullptr, none, (const int32_t*)nullptr, S, Hq, 0, n_items);
+    } else {
+        hipLaunchKernelGGL((qknorm_rope_append_kernel<bf16_t, DenseRows>), dim3((unsigned)blocks), dim3(256), 0, st,
+                           (const bf16_t*)q, q_row_stride, (const bf16_t*)q_norm_w, (const bf16_t*)nullptr, eps,
+                           order, (const bf16_t*)cos, (const bf16_t*)sin, cs_stride, table_rows, positions,
+                           (bf16_t*)q_out, (bf16_t*)nullptr, (bf16_t*)nullptr, none, (const int32_t*)nullptr, S, Hq, 0,
+                           n_items);
+    }
+    return launch_status(hipGetLastError());
+}
+
 extern "C" int crane_hip_qknorm_rope_append_paged(const void* qkv, int64_t qkv_row_stride, const void* q_norm_w,
                                                   const void* k_norm_w, float eps, int order, const void* cos,
                                                   const void* sin, int64_t cs_stride, int64_t table_rows,

@@ -85,6 +85,22 @@ def rope_tables(head_dim: int, theta: float, max_pos: int, alpha: float = 0.0,
     return freqs.cos().to(dtype).contiguous(), freqs.sin().to(dtype).contiguous()
 
 
+def rope_tables_qwen2(head_dim: int, theta: float, max_pos: int, device: torch.device | str = "cuda",
+                      dtype: torch.dtype = torch.float32):
+    """cos/sin tables [max_pos, head_dim/2] in candle-transformers qwen2's form
+    (copy at qwen25/qwen2.rs:47-64): inv_freq = 1 / theta^(2i/d) (f32) and the
+    positions are cast to the model dtype before the k=1 product, whose result
+    is rounded to the model dtype, and cos/sin are computed in f32 and rounded.
+    In bf16 this rounds positions above 256 and the angles themselves; in f32
+    it equals rope_tables.  Built on the host once per model."""
+    powers = torch.tensor([float(theta) ** (i / head_dim) for i in range(0, head_dim, 2)], dtype=torch.float64)
+    inv = (torch.ones((), dtype=torch.float32) / powers.to(torch.float32)).to(dtype)
+    pos = torch.arange(max_pos, dtype=torch.float32).to(dtype)
+    # a product of two bf16 values is exact in f32, so this is the one rounding of candle's matmul
+    freqs = (pos.float()[:, None] * inv.float()[None, :]).to(dtype).float()
+    return (freqs.cos().to(dtype).contiguous().to(device), freqs.sin().to(dtype).contiguous().to(device))
+
+
 # ------------------------------------------------------------ fused append op
 
 def qk_norm_rope_append(qkv: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,
@@ -132,6 +148,42 @@ def qk_norm_rope_append(qkv: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,
         q_out.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), k_cache.shape[2],
         cache_len.data_ptr(), max_rows, B, S, num_heads, num_kv_heads, D, dt, _stream(dev))
     check(rc, "qk_norm_rope_append")
+    return q_out
+
+
+def q_norm_rope(q: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, positions: torch.Tensor,
+                num_heads: int, q_norm_w: Optional[torch.Tensor] = None, eps: float = 1e-6,
+                order: str = "rope_then_norm") -> torch.Tensor:
+    """RoPE and the per-head query norm of a layer that reuses another layer's
+    K/V: Hunyuan's CLA path (hunyuan_dense/modeling.rs:502-514), q = rope(q)
+    then query_layernorm.  q is [B, S, Hq*D] (rows may be a narrowed view with
+    a unit inner stride); returns [B, Hq, S, D] for the attention ops, which
+    then read the anchor layer's cache."""
+    dev = _dev(q, cos, sin, positions, q_norm_w)
+    if q.dim() != 3:
+        raise CraneHipError(_lib.E_INVALID, "q must be [B, S, Hq*D]")
+    B, S, W = q.shape
+    D = HEAD_DIM
+    if W != num_heads * D:
+        raise CraneHipError(_lib.E_INVALID, f"q last dim {W} != Hq*{D}")
+    dt = _dtype_code(q)
+    for t, name in ((cos, "cos"), (sin, "sin"), (q_norm_w, "q_norm_w")):
+        if t is not None and t.dtype != q.dtype:
+            raise CraneHipError(_lib.E_DTYPE, f"{name} dtype {t.dtype} != q dtype {q.dtype}")
+    if q.stride(2) != 1 or q.stride(0) != S * q.stride(1):
+        raise CraneHipError(_lib.E_INVALID, "q rows must be dense with a unit inner stride")
+    _contig(cos, "cos")
+    _contig(sin, "sin")
+    if cos.shape != sin.shape or cos.dim() != 2 or cos.shape[1] != D // 2:
+        raise CraneHipError(_lib.E_INVALID, "cos/sin must be [max_pos, D/2]")
+    _i32(positions, B, "positions")
+    if order not in _ORDERS:
+        raise CraneHipError(_lib.E_INVALID, f"order {order!r}")
+    q_out = torch.empty((B, num_heads, S, D), dtype=q.dtype, device=dev)
+    rc = _lib.lib().crane_hip_qnorm_rope(
+        q.data_ptr(), q.stride(1), _ptr(q_norm_w), eps, _ORDERS[order], cos.data_ptr(), sin.data_ptr(),
+        cos.stride(0), cos.shape[0], positions.data_ptr(), q_out.data_ptr(), B, S, num_heads, D, dt, _stream(dev))
+    check(rc, "q_norm_rope")
     return q_out
 
 

@@ -96,6 +96,22 @@ int crane_hip_qknorm_rope_append(const void* qkv, int64_t qkv_row_stride,
                                  int64_t max_rows, int B, int S, int Hq, int Hkv, int D,
                                  int dtype, void* stream);
 
+/* Query-only QK-norm + RoPE for a layer that shares another layer's K/V:
+ * Hunyuan's cross-layer attention (CLA) path, hunyuan_dense/modeling.rs:502-514,
+ * which projects q alone, applies rope then query_layernorm, and attends over
+ * the anchor layer's cache (already appended for these tokens).  The same
+ * per-head arithmetic as crane_hip_qknorm_rope_append's q rows; no cache is
+ * read or written.
+ *
+ * q         [B, S, Hq*D] rows (row r at q + r*q_row_stride elements)
+ * q_norm_w  [D] or NULL (weight 1); order as above (Hunyuan: ROPE_THEN_NORM)
+ * q_out     [B, Hq, S, D]; the attention launchers then take the anchor's
+ *           cache and lengths. */
+int crane_hip_qnorm_rope(const void* q, int64_t q_row_stride, const void* q_norm_w, float eps, int order,
+                         const void* cos, const void* sin, int64_t cs_stride, int64_t table_rows,
+                         const int32_t* positions, void* q_out, int B, int S, int Hq, int D, int dtype,
+                         void* stream);
+
 /* Bytes of workspace crane_hip_attn_decode needs for these sizes (max_kv is
  * the largest kv_len the call may see). */
 size_t crane_hip_attn_decode_workspace(int B, int Hq, int Hkv, int D, int64_t max_kv, int dtype);

@@ -144,6 +144,34 @@ def test_append_argument_checks(kw, code):
     assert _append(**kw) == code
 
 
+def _qnorm(**kw):
+    a = dict(q=16, stride=2048, qw=None, eps=1e-6, order=1, cos=16, sin=16, cs_stride=64, rows=40960, pos=16,
+             q_out=16, B=1, S=2048, Hq=16, D=128, dtype=1, stream=None)
+    a.update(kw)
+    return _lib.lib().crane_hip_qnorm_rope(
+        a["q"], a["stride"], a["qw"], a["eps"], a["order"], a["cos"], a["sin"], a["cs_stride"], a["rows"], a["pos"],
+        a["q_out"], a["B"], a["S"], a["Hq"], a["D"], a["dtype"], a["stream"])
+
+
+@pytest.mark.parametrize("kw,code", [
+    (dict(dtype=2), _lib.E_DTYPE),
+    (dict(D=64), _lib.E_HEAD_DIM),
+    (dict(Hq=0), _lib.E_INVALID),
+    (dict(order=-1), _lib.E_INVALID),
+    (dict(stride=2000), _lib.E_INVALID),       # narrower than Hq*D
+    (dict(stride=2050), _lib.E_ALIGN),
+    (dict(cs_stride=60), _lib.E_INVALID),
+    (dict(q_out=None), _lib.E_INVALID),
+    (dict(pos=None), _lib.E_INVALID),
+    (dict(qw=24), _lib.E_ALIGN),
+    (dict(eps=float("nan")), _lib.E_INVALID),
+    (dict(B=0), _lib.OK),
+    (dict(S=0), _lib.OK),
+])
+def test_qnorm_rope_argument_checks(kw, code):
+    assert _qnorm(**kw) == code
+
+
 def test_ops_reject_cpu_tensors():
     import torch
     from crane_amd import ops

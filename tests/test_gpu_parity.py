@@ -174,6 +174,45 @@ def test_append_parity(gpu, orc, name, B, S, Hq, Hkv, clen, posn, cap, order, dt
     assert np.all(kg.transpose(0, 2, 1, 3)[untouched] == canary)
 
 
+@pytest.mark.parametrize("dtype", ["bf16", "f32"])
+def test_cla_q_only_matches_the_append(gpu, orc, dtype):
+    """Hunyuan's CLA layer: q alone through rope then query_layernorm, read
+    from a narrowed [B, S, Hq*D] view of a wider row, equals the q rows of the
+    full append bit for bit and the oracle's q within the bar; decode over the
+    anchor's cache with it matches the oracle."""
+    from crane_amd import ops
+    B, S, Hq, Hkv, cap = 3, 17, 8, 2, 64
+    note(f"cla q-only {dtype}: B={B} S={S} Hq={Hq}")
+    r = cases.rng(cases.SEED0 + 777)
+    qkv = cases.cast(cases.normal(r, (B, S, (Hq + 2 * Hkv) * D)), dtype)
+    qw = cases.cast(1 + 0.1 * cases.normal(r, (D,)), dtype)
+    kw = cases.cast(1 + 0.1 * cases.normal(r, (D,)), dtype)
+    cos, sin = (cases.cast(t, dtype) for t in orc.rope_tables(D, 1e6, 256))
+    clen, posn = [0, 4, 9], [0, 4, 30]
+    kc = np.zeros((B, Hkv, cap, D), np.float32)
+    vc = np.zeros((B, Hkv, cap, D), np.float32)
+    kd, vd = dev_t(kc, dtype, gpu), dev_t(vc, dtype, gpu)
+    qkv_d = dev_t(qkv, dtype, gpu)
+    cos_d, sin_d, pos_d, qw_d = dev_t(cos, dtype, gpu), dev_t(sin, dtype, gpu), i32(posn, gpu), dev_t(qw, dtype, gpu)
+    q_full = ops.qk_norm_rope_append(qkv_d, cos_d, sin_d, pos_d, kd, vd, i32(clen, gpu), max(clen) + S, Hq, Hkv,
+                                     qw_d, dev_t(kw, dtype, gpu), 1e-6, "rope_then_norm")
+    q_only = ops.q_norm_rope(qkv_d[:, :, :Hq * D], cos_d, sin_d, pos_d, Hq, qw_d, 1e-6, "rope_then_norm")
+    torch.cuda.synchronize()
+    assert torch.equal(q_only, q_full)
+    q_ref = orc.qk_norm_rope_append(qkv, Hq, Hkv, cos, sin, np.array(posn, np.int32), kc, vc,
+                                    np.array(clen, np.int32), qw, kw, 1e-6, 1, dtype)
+    assert_ulp_close(host(q_only), q_ref, dtype, "cla q")
+    # a one-token CLA decode over the anchor's cache (its rows include the new tokens)
+    lens = [c + S for c in clen]
+    q1 = ops.q_norm_rope(qkv_d[:, S - 1:, :].contiguous()[:, :, :Hq * D], cos_d, sin_d, i32([p + S - 1 for p in posn], gpu), Hq, qw_d,
+                         1e-6, "rope_then_norm")
+    out = ops.attention_decode(q1.reshape(B, Hq, D), kd, vd, i32(lens, gpu), max(lens))
+    torch.cuda.synchronize()
+    ref = orc.attn_decode(q_ref[:, :, S - 1, :], host(kd), host(vd), np.array(lens, np.int32), 1 / math.sqrt(D),
+                          dtype)
+    assert_close(host(out).reshape(ref.shape), ref, dtype, "cla decode")
+
+
 # ----------------------------------------------------------------- prefill
 
 PREFILL_CASES = [

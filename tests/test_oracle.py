@@ -70,6 +70,26 @@ def test_rope_tables_qwen2_dtype(orc):
     assert np.max(np.abs(cb[199] - c[199])) > 0.1
 
 
+def test_rope_tables_qwen2_host_builder(orc):
+    """ops.rope_tables_qwen2 (the tables a Qwen2.5 model hands the append)
+    against the oracle's qwen2 chain: bf16 within one bf16 ulp and almost all
+    equal (the host cos may differ from glibc's in the last f32 bit before the
+    rounding), f32 within one f32 ulp."""
+    import torch
+    from crane_amd import ops
+    cb, sb = orc.rope_tables_qwen2(D, 1e6, 3000, "bf16")
+    tc, ts = ops.rope_tables_qwen2(D, 1e6, 3000, device="cpu", dtype=torch.bfloat16)
+    for got, ref in ((tc.float().numpy(), cb), (ts.float().numpy(), sb)):
+        assert np.max(np.abs(got - ref)) <= 2 ** -8
+        assert np.mean(got == ref) > 0.999
+    assert torch.equal(tc[256], tc[257])                       # positions rounded to bf16
+    cf, sf = orc.rope_tables_qwen2(D, 1e6, 3000, "f32")
+    tc, ts = ops.rope_tables_qwen2(D, 1e6, 3000, device="cpu", dtype=torch.float32)
+    for got, ref in ((tc.numpy(), cf), (ts.numpy(), sf)):
+        ulp = np.spacing(np.abs(ref)).astype(np.float64)
+        assert np.all(np.abs(got.astype(np.float64) - ref) <= ulp + 1e-45)
+
+
 # ----------------------------------------------------------------- rmsnorm
 
 @pytest.mark.parametrize("contiguous", [True, False])
