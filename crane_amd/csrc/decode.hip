@@ -46,9 +46,6 @@ namespace {
 #define CRANE_DECODE_CHUNK 256
 #endif
 constexpr int kChunk = CRANE_DECODE_CHUNK;  // keys per workgroup (128 or 256)
-#ifndef CRANE_DECODE_EARLYV
-#define CRANE_DECODE_EARLYV 0
-#endif
 #ifndef CRANE_DECODE_CL
 #define CRANE_DECODE_CL 1
 #endif
@@ -113,6 +110,9 @@ __device__ __forceinline__ void decode_item(
     constexpr bool kBf16 = std::is_same<T, bf16_t>::value;
     constexpr int kVecA = 16 * (int)sizeof(T) / 16;  // 16-byte loads per lane per K row (16 dims)
     constexpr int kVecC = 8 * (int)sizeof(T) / 16;   // 16-byte loads per lane per V row (8 dims)
+    // V row pairs held in registers for C: all of them, or for 8 heads (whose
+    // accumulators take 64 VGPRs) a ring of 4 refilled as pairs are consumed.
+    constexpr int kVRing = G >= 8 ? 4 : kPairsC;
     const int sub_per_kv = n_rep / G;
     const int kvh = gi / sub_per_kv;
     const int h0 = kvh * n_rep + (gi % sub_per_kv) * G;  // first q head of this group
@@ -161,19 +161,6 @@ __device__ __forceinline__ void decode_item(
     const __amdgpu_buffer_rsrc_t rv = make_rsrc(vc + (off < 0 ? 0 : off), nbytes);
     constexpr int kRowBytes = kHeadDim * (int)sizeof(T);
 
-#if CRANE_DECODE_EARLYV
-    // V rows for C, issued before phase A: pairs m = w kChunk/8 + 4t + grp.
-    uint4 vr[kPairsC][2][kVecC];
-#pragma unroll
-    for (int t = 0; t < kPairsC; ++t) {
-        const int m = wave * (kChunk / 8) + 4 * t + grp;
-#pragma unroll
-        for (int r = 0; r < 2; ++r)
-#pragma unroll
-            for (int v = 0; v < kVecC; ++v)
-                vr[t][r][v] = buf_load16(rv, (2 * m + r) * kRowBytes + 16 * (kVecC * l16 + v));
-    }
-#endif
     // ---- A: raw scores q_g . k; wave w owns keys [w kChunk/4, (w+1) kChunk/4), 8 per load instruction
 #pragma unroll
     for (int half = 0; half < kStepsA / kKRows; ++half) {
@@ -209,11 +196,11 @@ __device__ __forceinline__ void decode_item(
         }
     }
 
-#if !CRANE_DECODE_EARLYV
-    // Prefetch this lane's V rows for C while B runs: pairs m = w kChunk/8 + 4t + grp.
-    uint4 vr[kPairsC][2][kVecC];
+    // Prefetch this lane's first V row pairs for C while B runs: pair m =
+    // w kChunk/8 + 4t + grp is rows 2m and 2m+1.
+    uint4 vr[kVRing][2][kVecC];
 #pragma unroll
-    for (int t = 0; t < kPairsC; ++t) {
+    for (int t = 0; t < kVRing; ++t) {
         const int m = wave * (kChunk / 8) + 4 * t + grp;
 #pragma unroll
         for (int r = 0; r < 2; ++r)
@@ -221,7 +208,6 @@ __device__ __forceinline__ void decode_item(
             for (int v = 0; v < kVecC; ++v)
                 vr[t][r][v] = buf_load16(rv, (2 * m + r) * kRowBytes + 16 * (kVecC * l16 + v));
     }
-#endif
     __syncthreads();
 
     // ---- B: per-head chunk max and sum (log2 domain); probabilities to LDS
@@ -268,13 +254,21 @@ __device__ __forceinline__ void decode_item(
         const int m = wave * (kChunk / 8) + 4 * t + grp;
         if constexpr (kBf16) {
             // interleave rows 2m and 2m+1 per dim: (v_2m[d], v_2m+1[d])
-            const uint32_t* r0 = reinterpret_cast<const uint32_t*>(&vr[t][0][0]);
-            const uint32_t* r1 = reinterpret_cast<const uint32_t*>(&vr[t][1][0]);
+            const uint32_t* r0 = reinterpret_cast<const uint32_t*>(&vr[t % kVRing][0][0]);
+            const uint32_t* r1 = reinterpret_cast<const uint32_t*>(&vr[t % kVRing][1][0]);
             uint32_t vv[8];
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 vv[2 * i] = __builtin_amdgcn_perm(r1[i], r0[i], 0x05040100u);      // low halves
                 vv[2 * i + 1] = __builtin_amdgcn_perm(r1[i], r0[i], 0x07060302u);  // high halves
+            }
+            if (t + kVRing < kPairsC) {  // refill the ring slot just consumed
+                const int m2 = wave * (kChunk / 8) + 4 * (t + kVRing) + grp;
+#pragma unroll
+                for (int r = 0; r < 2; ++r)
+#pragma unroll
+                    for (int v = 0; v < kVecC; ++v)
+                        vr[t % kVRing][r][v] = buf_load16(rv, (2 * m2 + r) * kRowBytes + 16 * (kVecC * l16 + v));
             }
             const uint32_t* pp = p_lds + m * G;
 #pragma unroll
@@ -286,7 +280,7 @@ __device__ __forceinline__ void decode_item(
         } else {
 #pragma unroll
             for (int r = 0; r < 2; ++r) {
-                const float* vf = reinterpret_cast<const float*>(&vr[t][r][0]);
+                const float* vf = reinterpret_cast<const float*>(&vr[t % kVRing][r][0]);
                 const float* pp = pf_lds + (2 * m + r) * G;
 #pragma unroll
                 for (int h = 0; h < G; ++h) {
@@ -294,6 +288,14 @@ __device__ __forceinline__ void decode_item(
 #pragma unroll
                     for (int d = 0; d < 8; ++d) o[h][d] += p * vf[d];
                 }
+            }
+            if (t + kVRing < kPairsC) {  // refill the ring slot just consumed
+                const int m2 = wave * (kChunk / 8) + 4 * (t + kVRing) + grp;
+#pragma unroll
+                for (int r = 0; r < 2; ++r)
+#pragma unroll
+                    for (int v = 0; v < kVecC; ++v)
+                        vr[t % kVRing][r][v] = buf_load16(rv, (2 * m2 + r) * kRowBytes + 16 * (kVecC * l16 + v));
             }
         }
     }
@@ -347,62 +349,67 @@ __global__ __launch_bounds__(kThreads) void decode_chunk_kernel(
                             ws_ml, out);
 }
 
-// Kernel 2: log-sum-exp merge of one (sequence, q head)'s partials; thread d
-// owns output dim d.  After kv_len, every load is issued at once: lane c loads
-// the (m, l) pair of split c while each thread loads the first kMergeRegs
-// partials of its dim into registers, so the merge costs one memory round
-// trip for up to kMergeRegs splits (4096 keys at 256 keys per split).
+// Kernel 2: log-sum-exp merge of one (sequence, q head)'s partials.  Thread
+// (p, d) owns output dim d for splits p, p + P, p + 2P, ...  After kv_len,
+// every load is issued at once: each thread loads its first kMergeRegs
+// partials into registers while the block reduces the (m, l) pairs, so up to
+// P * kMergeRegs splits (P * 4096 keys) cost one memory round trip.  P = 1
+// covers sequences up to 4096 keys; longer ones use P = 4, whose partition
+// sums meet in LDS.
 constexpr int kMergeRegs = 16;
-template <typename T>
-__global__ __launch_bounds__(kHeadDim) void decode_merge_kernel(
+template <typename T, int P>
+__global__ __launch_bounds__(kHeadDim * P) void decode_merge_kernel(
     const float* __restrict__ ws_o, const float* __restrict__ ws_ml, const int32_t* __restrict__ kv_len,
     int max_kv, int Hq, int nsplit, T* __restrict__ out) {
-    constexpr int chunk = kChunk;
+    constexpr int kWaves = kHeadDim * P / 64;
     __shared__ float w_lds[kMaxSplits];
-    __shared__ float red[2];
+    __shared__ float red[kWaves];
+    __shared__ float part[P > 1 ? P - 1 : 1][kHeadDim];
     const int bh = blockIdx.x;
     const int b = bh / Hq;
-    const int d = threadIdx.x;
+    const int tid = threadIdx.x;
+    const int d = tid % kHeadDim, p = tid / kHeadDim;
     const int L = min(kv_len[b], max_kv);
-    const int nc = (L + chunk - 1) / chunk;
+    const int nc = (L + kChunk - 1) / kChunk;
     if (nc <= 1) return;  // written by the split kernel
     const float* pm = ws_ml + (int64_t)bh * nsplit * 2;
     const float* po = ws_o + (int64_t)bh * nsplit * kHeadDim + d;
     float x[kMergeRegs];
 #pragma unroll
-    for (int i = 0; i < kMergeRegs; ++i) x[i] = i < nc ? po[(int64_t)i * kHeadDim] : 0.f;
+    for (int i = 0; i < kMergeRegs; ++i) x[i] = p + P * i < nc ? po[(int64_t)(p + P * i) * kHeadDim] : 0.f;
     float mx = -INFINITY;
-    for (int cc = d; cc < nc; cc += kHeadDim) mx = fmaxf(mx, pm[2 * cc]);
-    mx = fmaxf(mx, __shfl_xor(mx, 1));
-    mx = fmaxf(mx, __shfl_xor(mx, 2));
-    mx = fmaxf(mx, __shfl_xor(mx, 4));
-    mx = fmaxf(mx, __shfl_xor(mx, 8));
-    mx = fmaxf(mx, __shfl_xor(mx, 16));
-    mx = fmaxf(mx, __shfl_xor(mx, 32));
-    if ((d & 63) == 0) red[d >> 6] = mx;
+    for (int cc = tid; cc < nc; cc += kHeadDim * P) mx = fmaxf(mx, pm[2 * cc]);
+    mx = wave_max(mx);
+    if ((tid & 63) == 0) red[tid >> 6] = mx;
     __syncthreads();
-    const float M = fmaxf(red[0], red[1]);
+    float M = red[0];
+#pragma unroll
+    for (int w = 1; w < kWaves; ++w) M = fmaxf(M, red[w]);
     float den = 0.f;
-    for (int cc = d; cc < nc; cc += kHeadDim) {
+    for (int cc = tid; cc < nc; cc += kHeadDim * P) {
         const float w = fast_exp2(pm[2 * cc] - M);
         w_lds[cc] = w;
         den += w * pm[2 * cc + 1];
     }
-    den += __shfl_xor(den, 1);
-    den += __shfl_xor(den, 2);
-    den += __shfl_xor(den, 4);
-    den += __shfl_xor(den, 8);
-    den += __shfl_xor(den, 16);
-    den += __shfl_xor(den, 32);
+    den = wave_sum(den);
     __syncthreads();  // w_lds complete; red[] reads of the max are done
-    if ((d & 63) == 0) red[d >> 6] = den;
+    if ((tid & 63) == 0) red[tid >> 6] = den;
     __syncthreads();
-    den = red[0] + red[1];
+    den = red[0];
+#pragma unroll
+    for (int w = 1; w < kWaves; ++w) den += red[w];
     float num = 0.f;
 #pragma unroll
     for (int i = 0; i < kMergeRegs; ++i)
-        if (i < nc) num += w_lds[i] * x[i];
-    for (int cc = kMergeRegs; cc < nc; ++cc) num += w_lds[cc] * po[(int64_t)cc * kHeadDim];
+        if (p + P * i < nc) num += w_lds[p + P * i] * x[i];
+    for (int cc = p + P * kMergeRegs; cc < nc; cc += P) num += w_lds[cc] * po[(int64_t)cc * kHeadDim];
+    if constexpr (P > 1) {
+        if (p > 0) part[p - 1][d] = num;
+        __syncthreads();
+        if (p > 0) return;
+#pragma unroll
+        for (int q = 0; q < P - 1; ++q) num += part[q][d];
+    }
     Elem<T>::store(out + (int64_t)bh * kHeadDim + d, num / den);
 }
 
@@ -446,8 +453,11 @@ int launch_decode(const T* q, const T* kc, const T* vc, const ROWS& rows, const 
         default: return CRANE_HIP_E_GQA;
     }
     if (rc != CRANE_HIP_OK) return rc;
-    if (nsplit > 1)
-        hipLaunchKernelGGL(decode_merge_kernel<T>, dim3((unsigned)(B * Hq)), dim3(kHeadDim), 0, st, ws_o, ws_ml,
+    if (nsplit > kMergeRegs)
+        hipLaunchKernelGGL((decode_merge_kernel<T, 4>), dim3((unsigned)(B * Hq)), dim3(kHeadDim * 4), 0, st, ws_o,
+                           ws_ml, kv_len, max_kv, Hq, nsplit, out);
+    else if (nsplit > 1)
+        hipLaunchKernelGGL((decode_merge_kernel<T, 1>), dim3((unsigned)(B * Hq)), dim3(kHeadDim), 0, st, ws_o, ws_ml,
                            kv_len, max_kv, Hq, nsplit, out);
     return launch_status(hipGetLastError());
 }
