@@ -16,7 +16,11 @@
 //   A. scores: 8 lanes read one K row (two 16-byte loads each, 16 dims per
 //      lane; a wave covers 8 rows per load pair), each lane does the dot
 //      product of its 16 dims with v_dot2_f32_bf16 for all G heads, and a
-//      3-step DPP butterfly inside the 8 lanes completes it.
+//      3-step DPP butterfly inside the 8 lanes completes it.  Lane a of the 8
+//      reads bytes [16a, 16a+16) and [128+16a, 128+16a+16) of the row, so
+//      each load instruction covers whole 128-byte lines (the q dims follow
+//      the same map); pieces 32 bytes apart would touch every line twice,
+//      which measured 5% (8 heads: 9%) slower.
 //   B. the chunk's softmax statistics per head (max m and sum l of the
 //      bf16-rounded exp2(s - m), log2 domain), computed once per (head, key)
 //      with DPP wave reductions; probabilities go to LDS as packed bf16 pairs
@@ -141,9 +145,15 @@ __device__ __forceinline__ void decode_item(
 #pragma unroll
     for (int h = 0; h < G; ++h) {
         float x[16];
-        const T* qh = q + ((int64_t)b * Hq + h0 + h) * kHeadDim + 16 * a8;
-        load8(qh, *reinterpret_cast<float(*)[8]>(&x[0]));
-        load8(qh + 8, *reinterpret_cast<float(*)[8]>(&x[8]));
+        // the lane's dims are those of its K pieces: bytes [128 v + 16 a8, +16) of the row
+        const T* qr = q + ((int64_t)b * Hq + h0 + h) * kHeadDim;
+        if constexpr (kBf16) {
+            load8(qr + 8 * a8, *reinterpret_cast<float(*)[8]>(&x[0]));
+            load8(qr + 64 + 8 * a8, *reinterpret_cast<float(*)[8]>(&x[8]));
+        } else {
+#pragma unroll
+            for (int v = 0; v < 4; ++v) load4(qr + 32 * v + 4 * a8, *reinterpret_cast<float(*)[4]>(&x[4 * v]));
+        }
         if constexpr (kBf16) {
 #pragma unroll
             for (int i = 0; i < 8; ++i) qp[h][i] = pack_bf16x2(x[2 * i] * scale_t, x[2 * i + 1] * scale_t);
@@ -169,7 +179,7 @@ __device__ __forceinline__ void decode_item(
         for (int t = 0; t < kKRows; ++t) {
             const int j = wave * (kChunk / 4) + (half * kKRows + t) * 8 + r8;
 #pragma unroll
-            for (int v = 0; v < kVecA; ++v) kr[t][v] = buf_load16(rk, j * kRowBytes + 16 * (kVecA * a8 + v));
+            for (int v = 0; v < kVecA; ++v) kr[t][v] = buf_load16(rk, j * kRowBytes + 128 * v + 16 * a8);
         }
 #pragma unroll
         for (int t = 0; t < kKRows; ++t) {
