@@ -50,6 +50,9 @@ DECODE_CASES = [
     ("qwen25_7b_gqa7_bf16", 4, 28, 4, [100, 1500, 4096, 33], "bf16", 1.0),
     ("gqa16_bf16", 2, 32, 2, [513, 2000], "bf16", 1.0),
     ("gqa3_f32", 2, 6, 2, [40, 900], "f32", 1.0),
+    # max_kv past 12288: 512-key chunks and the 4-partition merge
+    ("long_chunks_f32", 2, 8, 2, [13000, 20001], "f32", 1.0),
+    ("long_chunks_ragged_bf16", 3, 16, 2, [12289, 15000, 700], "bf16", 1.0),
 ]
 
 

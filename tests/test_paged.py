@@ -125,6 +125,30 @@ def test_paged_decode_equals_dense(gpu, dtype, page_rows, Hq, Hkv):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("page_rows", [512, 256])
+def test_paged_decode_long_context(gpu, orc, page_rows):
+    """Past 12288 keys the dense launcher takes 512-key chunks; so does the
+    paged one when a page holds whole 512-row chunks (then the two are
+    bit-equal), and 256-row pages keep 256-key chunks (checked against the
+    oracle)."""
+    import torch
+    from crane_amd import ops
+    lens = np.array([12289, 14000, 600], np.int32)
+    print(f"paged decode long P={page_rows}", flush=True)
+    q, k, v, lens = cases.decode_case(9300 + page_rows, len(lens), 16, 2, lens, dtype="bf16")
+    kp, vp, table, _ = to_paged(k, v, lens, page_rows, seed=19)
+    kvl = torch.as_tensor(lens, device=gpu)
+    got = ops.attention_decode_paged(_t(q, "bf16", gpu), _t(kp, "bf16", gpu), _t(vp, "bf16", gpu),
+                                     torch.as_tensor(table, device=gpu), kvl, int(lens.max()))
+    assert not torch.isnan(got).any()
+    if page_rows % 512 == 0:
+        want = ops.attention_decode(_t(q, "bf16", gpu), _t(k, "bf16", gpu), _t(v, "bf16", gpu), kvl, int(lens.max()))
+        assert torch.equal(got, want)
+    ref = orc.attn_decode(q, k, v, lens, cases.scale(), "bf16")
+    assert_close(got.float().cpu().numpy().reshape(ref.shape), ref, "bf16", f"paged long P={page_rows}")
+
+
+@pytest.mark.gpu
 @pytest.mark.parametrize("dtype,causal,start", [("bf16", True, [0, 0]), ("bf16", True, [200, 37]),
                                                 ("bf16", False, [64, 300]), ("f32", True, [5, 130])])
 def test_paged_prefill_equals_dense(gpu, dtype, causal, start):
