@@ -416,6 +416,48 @@ __global__ __launch_bounds__(kHeadDim * P) void decode_merge_kernel(
     Elem<T>::store(out + (int64_t)bh * kHeadDim + d, num / den);
 }
 
+// Kernel 2 for up to kMergeRegs splits: one wave per (sequence, q head), four
+// heads of a group per workgroup.  Lane l owns dims 2l and 2l+1 and lane c
+// holds split c's (m, l), so the max and the denominator are DPP wave
+// reductions and each split's weight reaches every lane by readlane: no LDS
+// and no barrier.  The sums run in the order of decode_merge_kernel<.., 1>.
+// grid (groups, B, ceil(G / 4)), as the chunk kernel's (groups, B).
+template <typename T, int CH>
+__global__ __launch_bounds__(256) void decode_merge_wave_kernel(
+    const float* __restrict__ ws_o, const float* __restrict__ ws_ml, const int32_t* __restrict__ kv_len,
+    int max_kv, int Hq, int n_rep, int G, int nsplit, T* __restrict__ out) {
+    const int lane = threadIdx.x & 63;
+    const int hh = (int)blockIdx.z * 4 + (threadIdx.x >> 6);
+    if (hh >= G) return;  // whole waves
+    const int sub = n_rep / G, gi = (int)blockIdx.x, b = (int)blockIdx.y;
+    const int bh = b * Hq + (gi / sub) * n_rep + (gi % sub) * G + hh;
+    const int L = min(kv_len[b], max_kv);
+    const int nc = (L + CH - 1) / CH;
+    if (nc <= 1) return;  // written by the split kernel
+    const float* pm = ws_ml + (int64_t)bh * nsplit * 2;
+    const float2* po = reinterpret_cast<const float2*>(ws_o + (int64_t)bh * nsplit * kHeadDim) + lane;
+    float2 x[kMergeRegs];
+#pragma unroll
+    for (int i = 0; i < kMergeRegs; ++i) x[i] = i < nc ? po[i * (kHeadDim / 2)] : make_float2(0.f, 0.f);
+    const float m = lane < nc ? pm[2 * lane] : -INFINITY;
+    const float l = lane < nc ? pm[2 * lane + 1] : 0.f;
+    const float M = wave_max(m);
+    const float w = lane < nc ? fast_exp2(m - M) : 0.f;
+    const float den = wave_sum(w * l);
+    float n0 = 0.f, n1 = 0.f;
+#pragma unroll
+    for (int i = 0; i < kMergeRegs; ++i) {
+        if (i < nc) {
+            const float wi = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, w), i));
+            n0 += wi * x[i].x;
+            n1 += wi * x[i].y;
+        }
+    }
+    T* o = out + (int64_t)bh * kHeadDim + 2 * lane;
+    Elem<T>::store(o, n0 / den);
+    Elem<T>::store(o + 1, n1 / den);
+}
+
 int pick_group(int n_rep) {
     for (int g = kMaxGroup; g >= 1; --g)
         if (n_rep % g == 0) return g;
@@ -463,8 +505,8 @@ int launch_decode(const T* q, const T* kc, const T* vc, const ROWS& rows, const 
         hipLaunchKernelGGL((decode_merge_kernel<T, CH, 4>), mgrid, dim3(kHeadDim * 4), 0, st, ws_o, ws_ml, kv_len,
                            max_kv, Hq, n_rep, nsplit, out);
     else if (nsplit > 1)
-        hipLaunchKernelGGL((decode_merge_kernel<T, CH, 1>), mgrid, dim3(kHeadDim), 0, st, ws_o, ws_ml, kv_len, max_kv,
-                           Hq, n_rep, nsplit, out);
+        hipLaunchKernelGGL((decode_merge_wave_kernel<T, CH>), dim3(mgrid.x, mgrid.y, (unsigned)((G + 3) / 4)), dim3(256),
+                           0, st, ws_o, ws_ml, kv_len, max_kv, Hq, n_rep, G, nsplit, out);
     return launch_status(hipGetLastError());
 }
 
