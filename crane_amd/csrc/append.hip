@@ -9,49 +9,53 @@
 // the Qwen2.5 order (rope only: qwen2.rs:75-76) selected by `order`.
 //
 // Work item = one head row (128 elements) of one token: Hq query rows, Hkv key
-// rows and Hkv value rows per token.  16 lanes own an item; lane l holds dims
-// [4l, 4l+4) and their rotate-half partners [64+4l, 64+4l+4), so the rotation
-// is lane-local and the RMS sum is a 16-lane butterfly.  The arithmetic is f32
-// with the result of every candle op rounded to the storage type, as Crane's
-// candle op chain rounds it (the kernel is HBM-bound, so this is free).  Every
-// cache row is written exactly once; q lands in [B,Hq,S,D] for the attention
-// kernels.  HBM traffic per token: (Hq+2Hkv)*D elements read, the same written.
+// rows and Hkv value rows per token.  8 lanes own an item; lane l holds dims
+// [8l, 8l+8) and their rotate-half partners [64+8l, 64+8l+8) as two 16-byte
+// pieces, so the rotation is lane-local and the RMS sum is an 8-lane DPP
+// butterfly.  The arithmetic is f32 with the result of every candle op
+// rounded to the storage type, as Crane's candle op chain rounds it (the
+// kernel is HBM-bound, so this is free).  Every cache row is written exactly
+// once; q lands in [B,Hq,S,D] for the attention kernels.
+// HBM traffic per token: (Hq+2Hkv)*D elements read, the same written.
 #include "common.h"
 
 namespace crane {
 namespace {
 
-constexpr int kItemsPerBlock = 16;  // 256 threads / 16 lanes per item
+constexpr int kItemsPerBlock = 32;  // 256 threads / 8 lanes per item
 
-__device__ __forceinline__ float group16_sum(float v) {
-    v += __shfl_xor(v, 1, 16);
-    v += __shfl_xor(v, 2, 16);
-    v += __shfl_xor(v, 4, 16);
-    v += __shfl_xor(v, 8, 16);
-    return v;
+// Sum over the 8 lanes of a DPP half-row; every lane gets the total.
+__device__ __forceinline__ float group8_sum(float x) {
+    x += dpp<0xB1>(x);   // quad_perm [1,0,3,2]
+    x += dpp<0x4E>(x);   // quad_perm [2,3,0,1]
+    x += dpp<0x141>(x);  // row_half_mirror
+    return x;
 }
 
-// candle_nn RmsNorm over the 128 dims held by 16 lanes.  `contiguous` selects
+// candle_nn RmsNorm over the 128 dims held by 8 lanes.  `contiguous` selects
 // candle's fused ops::rms_norm (m = sqrt(mean(x^2)+eps) converted to T, then
 // x / m * w in T) or the LayerNorm fallback used for a non-contiguous input
 // (x / sqrt(mean(x^2)+eps) in f32, converted to T, then * w in T).  The sum of
 // squares accumulates in f32.
 template <typename T>
-__device__ __forceinline__ void rms_norm16(float (&x1)[4], float (&x2)[4], const T* w, int l, float eps,
-                                           bool contiguous) {
+__device__ __forceinline__ void rms_norm8(float (&x1)[8], float (&x2)[8], const T* w, int l, float eps,
+                                          bool contiguous) {
     float ss = 0.f;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) ss += x1[i] * x1[i] + x2[i] * x2[i];
-    ss = group16_sum(ss);
+    for (int i = 0; i < 8; ++i) ss += x1[i] * x1[i] + x2[i] * x2[i];
+    ss = group8_sum(ss);
     float m = sqrtf(ss * (1.0f / kHeadDim) + eps);
     if (contiguous) m = rt<T>(m);
-    float w1[4] = {1.f, 1.f, 1.f, 1.f}, w2[4] = {1.f, 1.f, 1.f, 1.f};
+    float w1[8], w2[8];
     if (w) {
-        load4(w + 4 * l, w1);
-        load4(w + 64 + 4 * l, w2);
+        load8(w + 8 * l, w1);
+        load8(w + 64 + 8 * l, w2);
+    } else {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) w1[i] = w2[i] = 1.f;
     }
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < 8; ++i) {
         x1[i] = rt<T>(rt<T>(x1[i] / m) * w1[i]);
         x2[i] = rt<T>(rt<T>(x2[i] / m) * w2[i]);
     }
@@ -59,10 +63,10 @@ __device__ __forceinline__ void rms_norm16(float (&x1)[4], float (&x2)[4], const
 
 // candle_nn::rotary_emb::rope (rotate-half): every product and sum rounded in T.
 template <typename T>
-__device__ __forceinline__ void rope4(float (&x1)[4], float (&x2)[4], const float (&c)[4], const float (&s)[4]) {
+__device__ __forceinline__ void rope8(float (&x1)[8], float (&x2)[8], const float (&c)[8], const float (&s)[8]) {
 #pragma clang fp contract(off)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < 8; ++i) {
         const float a = x1[i], b = x2[i];
         x1[i] = rt<T>(rt<T>(a * c[i]) - rt<T>(b * s[i]));
         x2[i] = rt<T>(rt<T>(a * s[i]) + rt<T>(b * c[i]));
@@ -76,9 +80,9 @@ __global__ __launch_bounds__(256) void qknorm_rope_append_kernel(
     int64_t table_rows, const int32_t* __restrict__ positions, T* __restrict__ q_out, T* __restrict__ k_cache,
     T* __restrict__ v_cache, ROWS rows, const int32_t* __restrict__ cache_len, int S, int Hq, int Hkv,
     int64_t n_items) {
-    const int64_t item = (int64_t)blockIdx.x * kItemsPerBlock + (threadIdx.x >> 4);
-    const int l = threadIdx.x & 15;
-    if (item >= n_items) return;  // whole 16-lane groups leave together
+    const int64_t item = (int64_t)blockIdx.x * kItemsPerBlock + (threadIdx.x >> 3);
+    const int l = threadIdx.x & 7;
+    if (item >= n_items) return;  // whole 8-lane groups leave together
     const int H = Hq + 2 * Hkv;
     const int head = (int)(item % H);
     const int64_t tok = item / H;
@@ -86,16 +90,16 @@ __global__ __launch_bounds__(256) void qknorm_rope_append_kernel(
     const int b = (int)(tok / S);
 
     const T* src = qkv + tok * row_stride + (int64_t)head * kHeadDim;
-    float x1[4], x2[4];
-    load4(src + 4 * l, x1);
-    load4(src + 64 + 4 * l, x2);
+    float x1[8], x2[8];
+    load8(src + 8 * l, x1);
+    load8(src + 64 + 8 * l, x2);
 
     if (head >= Hq + Hkv) {  // value row: straight into the cache
         const int64_t off = rows.offset(b, Hkv, head - Hq - Hkv, (int64_t)cache_len[b] + s);
         if (off < 0) return;  // past the capacity (or on an invalid page): not written
         T* dst = v_cache + off;
-        store4(dst + 4 * l, x1);
-        store4(dst + 64 + 4 * l, x2);
+        store8(dst + 8 * l, x1);
+        store8(dst + 64 + 8 * l, x2);
         return;
     }
     const bool is_q = head < Hq;
@@ -110,18 +114,18 @@ __global__ __launch_bounds__(256) void qknorm_rope_append_kernel(
     const T* w = is_q ? qw : kw;
     const int64_t p = (int64_t)positions[b] + s;
     if (p < 0 || p >= table_rows) return;  // no table row for this position: nothing is written
-    float c[4], sn[4];
-    load4(cos_t + p * cs_stride + 4 * l, c);
-    load4(sin_t + p * cs_stride + 4 * l, sn);
+    float c[8], sn[8];
+    load8(cos_t + p * cs_stride + 8 * l, c);
+    load8(sin_t + p * cs_stride + 8 * l, sn);
 
     // Qwen3 norms the transposed [B,H,S,D] view, contiguous only when S == 1;
     // Hunyuan norms the contiguous rope output.
-    if (order == CRANE_HIP_NORM_THEN_ROPE) rms_norm16(x1, x2, w, l, eps, S == 1);
-    rope4<T>(x1, x2, c, sn);
-    if (order == CRANE_HIP_ROPE_THEN_NORM) rms_norm16(x1, x2, w, l, eps, true);
+    if (order == CRANE_HIP_NORM_THEN_ROPE) rms_norm8(x1, x2, w, l, eps, S == 1);
+    rope8<T>(x1, x2, c, sn);
+    if (order == CRANE_HIP_ROPE_THEN_NORM) rms_norm8(x1, x2, w, l, eps, true);
 
-    store4(dst + 4 * l, x1);
-    store4(dst + 64 + 4 * l, x2);
+    store8(dst + 8 * l, x1);
+    store8(dst + 64 + 8 * l, x2);
 }
 
 // Checks shared by both layouts, then the launch; `rows` addresses the cache.
@@ -141,7 +145,8 @@ int qknorm_rope_append(const void* qkv, int64_t qkv_row_stride, const void* q_no
         return CRANE_HIP_E_INVALID;
     if (qkv_row_stride < (int64_t)(Hq + 2 * Hkv) * D || cs_stride < D / 2 || table_rows <= 0)
         return CRANE_HIP_E_INVALID;
-    if (qkv_row_stride % 4 != 0 || cs_stride % 4 != 0) return CRANE_HIP_E_ALIGN;
+    const int64_t per16 = dtype == CRANE_HIP_BF16 ? 8 : 4;  // elements per 16 bytes
+    if (qkv_row_stride % per16 != 0 || cs_stride % per16 != 0) return CRANE_HIP_E_ALIGN;
     if (!aligned16(qkv) || !aligned16(cos) || !aligned16(sin) || !aligned16(q_out) || !aligned16(k_cache) ||
         !aligned16(v_cache) || (q_norm_w && !aligned16(q_norm_w)) || (k_norm_w && !aligned16(k_norm_w)))
         return CRANE_HIP_E_ALIGN;
@@ -201,7 +206,8 @@ extern "C" int crane_hip_qnorm_rope(const void* q, int64_t q_row_stride, const v
     if (B == 0 || S == 0) return CRANE_HIP_OK;
     if (!q || !cos || !sin || !positions || !q_out) return CRANE_HIP_E_INVALID;
     if (q_row_stride < (int64_t)Hq * D || cs_stride < D / 2 || table_rows <= 0) return CRANE_HIP_E_INVALID;
-    if (q_row_stride % 4 != 0 || cs_stride % 4 != 0) return CRANE_HIP_E_ALIGN;
+    const int64_t per16 = dtype == CRANE_HIP_BF16 ? 8 : 4;  // elements per 16 bytes
+    if (q_row_stride % per16 != 0 || cs_stride % per16 != 0) return CRANE_HIP_E_ALIGN;
     if (!aligned16(q) || !aligned16(cos) || !aligned16(sin) || !aligned16(q_out) || (q_norm_w && !aligned16(q_norm_w)))
         return CRANE_HIP_E_ALIGN;
     const int64_t n_items = (int64_t)B * S * Hq;

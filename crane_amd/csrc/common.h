@@ -74,6 +74,16 @@ __device__ __forceinline__ void load8(const bf16_t* p, float (&v)[8]) {
     v[4] = bf16_lo(t.z); v[5] = bf16_hi(t.z); v[6] = bf16_lo(t.w); v[7] = bf16_hi(t.w);
 }
 
+// Store 8 consecutive elements.
+__device__ __forceinline__ void store8(float* p, const float (&v)[8]) {
+    *reinterpret_cast<float4*>(p) = make_float4(v[0], v[1], v[2], v[3]);
+    *reinterpret_cast<float4*>(p + 4) = make_float4(v[4], v[5], v[6], v[7]);
+}
+__device__ __forceinline__ void store8(bf16_t* p, const float (&v)[8]) {
+    *reinterpret_cast<uint4*>(p) =
+        make_uint4(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]), pack_bf16x2(v[4], v[5]), pack_bf16x2(v[6], v[7]));
+}
+
 // Rounding to the storage type after a candle op: identity for f32,
 // round-to-nearest-even bf16 for bf16 (half::bf16 arithmetic rounds every op).
 template <typename T> __device__ __forceinline__ float rt(float x);
