@@ -253,28 +253,33 @@ def bench_layer(args, dev, stream, lib):
     prefill rows (Qwen2.5-7B: 8 x 4096 rows, hidden 3584, intermediate 18944)
     and config 3's decode rows (Qwen3-8B: 32 rows, hidden 4096, intermediate
     12288).  Algorithmic bytes: every tensor read or written once (the norm
-    weight counted once)."""
+    weight counted once).  At config 4 the hidden-size tensors (235 MB each)
+    rotate through 3 copies, so a call's reads cannot come from the 256 MB
+    Infinity Cache left warm by the call before; silu_mul moves 3.7 GB a call."""
     import torch
     res = {}
     st = stream.cuda_stream
     for tag, rows, hidden, inter in (("c4_prefill_rows", 8 * 4096, 3584, 18944), ("c3_decode_rows", 32, 4096, 12288)):
         gen = torch.Generator(device=dev).manual_seed(SEED0 + 7)
-        x = randn((rows, hidden), gen, torch.bfloat16, dev)
-        h = randn((rows, hidden), gen, torch.bfloat16, dev)
+        R = 3 if rows >= 4096 else 1
+        xs = [randn((rows, hidden), gen, torch.bfloat16, dev) for _ in range(R)]
+        hs = [randn((rows, hidden), gen, torch.bfloat16, dev) for _ in range(R)]
         w = randn((hidden,), gen, torch.bfloat16, dev)
-        out = torch.empty_like(x)
+        outs = [torch.empty_like(xs[0]) for _ in range(R)]
         gu = randn((rows, 2 * inter), gen, torch.bfloat16, dev)
         act = torch.empty((rows, inter), dtype=torch.bfloat16, device=dev)
         row_bytes = hidden * 2
         ops_ = {
-            "rms_norm": (lambda i: lib.crane_hip_rms_norm(x.data_ptr(), w.data_ptr(), out.data_ptr(), rows, hidden,
-                                                           1e-6, 1, st), 2 * rows * row_bytes + row_bytes),
-            "add_rms_norm": (lambda i: lib.crane_hip_add_rms_norm(x.data_ptr(), h.data_ptr(), w.data_ptr(),
-                                                                   out.data_ptr(), rows, hidden, 1e-6, 1, st),
+            "rms_norm": (lambda i: lib.crane_hip_rms_norm(xs[i % R].data_ptr(), w.data_ptr(), outs[i % R].data_ptr(),
+                                                           rows, hidden, 1e-6, 1, st), 2 * rows * row_bytes + row_bytes),
+            "add_rms_norm": (lambda i: lib.crane_hip_add_rms_norm(xs[i % R].data_ptr(), hs[i % R].data_ptr(),
+                                                                   w.data_ptr(), outs[i % R].data_ptr(), rows, hidden,
+                                                                   1e-6, 1, st),
                              4 * rows * row_bytes + row_bytes),
             "silu_mul": (lambda i: lib.crane_hip_silu_mul(gu.data_ptr(), act.data_ptr(), rows, inter, 1, st),
                          3 * rows * inter * 2),
-            "residual_add": (lambda i: lib.crane_hip_residual_add(x.data_ptr(), h.data_ptr(), rows * hidden, 1, st),
+            "residual_add": (lambda i: lib.crane_hip_residual_add(xs[i % R].data_ptr(), hs[i % R].data_ptr(),
+                                                                   rows * hidden, 1, st),
                              3 * rows * row_bytes),
         }
         res[tag] = {}
@@ -287,7 +292,7 @@ def bench_layer(args, dev, stream, lib):
             gbs = nbytes / (ms * 1e-3) / 1e9
             res[tag][name] = dict(us=ms * 1e3, gbs=gbs, frac=gbs / HBM_PEAK_GBS, bytes=nbytes)
             log(f"[layer {tag}] {name}: {ms * 1e3:.1f} us, {gbs:.0f} GB/s ({gbs / HBM_PEAK_GBS * 100:.1f}% of HBM)")
-        del x, h, out, gu, act
+        del xs, hs, outs, gu, act
         torch.cuda.empty_cache()
     return res
 
@@ -416,7 +421,9 @@ def bench_prefill_c2(args, dev, stream, lib):
 
 def bench_append(args, dev, stream, lib):
     """Fused QK-norm + RoPE + KV append at config 4's prefill size (8 x 4096
-    tokens, 28/4 heads, rope only) and config 3's decode step (32 tokens)."""
+    tokens, 28/4 heads, rope only) and config 3's decode step (32 tokens).  At
+    config 4 the inputs and outputs (670 MB a call) rotate through 2 copies, so
+    a call cannot read what the one before left in the 256 MB Infinity Cache."""
     import torch
     from crane_amd import ops
     res = {}
@@ -426,15 +433,17 @@ def bench_append(args, dev, stream, lib):
             "c4_prefill_append": (8, 4096, 28, 4, 2, 0),
             "c3_decode_append": (32, 1, 32, 8, 0, 4096)}.items():
         gen = torch.Generator(device=dev).manual_seed(SEED0 + 40)
-        qkv = randn((B, S, (Hq + 2 * Hkv) * D), gen, torch.bfloat16, dev)
+        R = 2 if S > 1 else 1
+        qkvs = [randn((B, S, (Hq + 2 * Hkv) * D), gen, torch.bfloat16, dev) for _ in range(R)]
         cap = start + S
-        kc = torch.zeros((B, Hkv, cap, D), dtype=torch.bfloat16, device=dev)
-        vc = torch.zeros_like(kc)
-        q_out = torch.empty((B, Hq, S, D), dtype=torch.bfloat16, device=dev)
+        kcs = [torch.zeros((B, Hkv, cap, D), dtype=torch.bfloat16, device=dev) for _ in range(R)]
+        vcs = [torch.zeros_like(kcs[0]) for _ in range(R)]
+        q_outs = [torch.empty((B, Hq, S, D), dtype=torch.bfloat16, device=dev) for _ in range(R)]
         pos = torch.full((B,), start, dtype=torch.int32, device=dev)
         w = torch.ones(D, dtype=torch.bfloat16, device=dev)
 
         def launch(i):
+            qkv, q_out, kc, vc = qkvs[i % R], q_outs[i % R], kcs[i % R], vcs[i % R]
             rc = lib.crane_hip_qknorm_rope_append(
                 qkv.data_ptr(), qkv.stride(1), w.data_ptr(), w.data_ptr(), 1e-6, order, cos.data_ptr(),
                 sin.data_ptr(), cos.stride(0), cos.shape[0], pos.data_ptr(), q_out.data_ptr(), kc.data_ptr(),

@@ -45,10 +45,31 @@ template <> struct Vec<bf16_t> {
     }
 };
 
-template <typename T>
-__device__ __forceinline__ uint4 ld16(const T* p) { return *reinterpret_cast<const uint4*>(p); }
-template <typename T>
-__device__ __forceinline__ void st16(T* p, const uint4& u) { *reinterpret_cast<uint4*>(p) = u; }
+// 16-byte loads and stores; NT selects the non-temporal (streaming) policy.
+// Which kernel streams what was measured at config 4's prefill rows with the
+// tensors rotated through 3 copies (so the 256 MB Infinity Cache cannot
+// serve a call from the one before): rms_norm 6% faster with non-temporal
+// stores, add + rms_norm and the residual add 8% faster with both,
+// silu_mul fastest with neither.
+typedef unsigned int u32x4_v __attribute__((ext_vector_type(4)));
+template <bool NT, typename T>
+__device__ __forceinline__ uint4 ld16(const T* p) {
+    if constexpr (NT) {
+        const u32x4_v v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_v*>(p));
+        return make_uint4(v.x, v.y, v.z, v.w);
+    } else {
+        return *reinterpret_cast<const uint4*>(p);
+    }
+}
+template <bool NT, typename T>
+__device__ __forceinline__ void st16(T* p, const uint4& u) {
+    if constexpr (NT) {
+        const u32x4_v v = {u.x, u.y, u.z, u.w};
+        __builtin_nontemporal_store(v, reinterpret_cast<u32x4_v*>(p));
+    } else {
+        *reinterpret_cast<uint4*>(p) = u;
+    }
+}
 
 constexpr int kRowsPerBlock = 4;  // one wave per row
 
@@ -58,6 +79,7 @@ __global__ __launch_bounds__(64 * kRowsPerBlock) void rms_norm_kernel(T* __restr
                                                                      const T* __restrict__ w, T* __restrict__ out,
                                                                      int64_t rows, int cols, float eps) {
     constexpr int N = Vec<T>::N;
+    constexpr bool kNtLoad = ADD;  // the rows are streamed; the weight is shared by all rows
     const int lane = threadIdx.x & 63;
     const int64_t row = (int64_t)blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
     if (row >= rows) return;  // whole waves
@@ -69,15 +91,15 @@ __global__ __launch_bounds__(64 * kRowsPerBlock) void rms_norm_kernel(T* __restr
     for (int i = 0; i < CH; ++i) {
         const int idx = i * 64 + lane;
         if (idx < nch) {
-            uint4 a = ld16(xr + idx * N);
+            uint4 a = ld16<kNtLoad>(xr + idx * N);
             if constexpr (ADD) {  // residual = T(residual + hidden), stored, and normed as rounded
                 float va[N], vh[N];
                 Vec<T>::unpack(a, va);
-                Vec<T>::unpack(ld16(hidden + row * cols + idx * N), vh);
+                Vec<T>::unpack(ld16<kNtLoad>(hidden + row * cols + idx * N), vh);
 #pragma unroll
                 for (int e = 0; e < N; ++e) va[e] += vh[e];
                 a = Vec<T>::pack(va);
-                st16(xr + idx * N, a);
+                st16<true>(xr + idx * N, a);
             }
             c[i] = a;
             float v[N];
@@ -96,14 +118,14 @@ __global__ __launch_bounds__(64 * kRowsPerBlock) void rms_norm_kernel(T* __restr
             float v[N], wv[N];
             Vec<T>::unpack(c[i], v);
             if (w) {
-                Vec<T>::unpack(ld16(w + idx * N), wv);
+                Vec<T>::unpack(ld16<false>(w + idx * N), wv);
             } else {
 #pragma unroll
                 for (int e = 0; e < N; ++e) wv[e] = 1.f;
             }
 #pragma unroll
             for (int e = 0; e < N; ++e) v[e] = rt<T>(v[e] / m) * wv[e];
-            st16(orow + idx * N, Vec<T>::pack(v));  // the pack rounds the product to T
+            st16<true>(orow + idx * N, Vec<T>::pack(v));  // the pack rounds the product to T
         }
     }
 }
@@ -121,11 +143,11 @@ __global__ __launch_bounds__(256) void silu_mul_kernel(const T* __restrict__ gu,
         const int j = (int)(c % cpr);
         const T* g = gu + r * 2 * inter + (int64_t)j * N;
         float gv[N], uv[N];
-        Vec<T>::unpack(ld16(g), gv);
-        Vec<T>::unpack(ld16(g + inter), uv);
+        Vec<T>::unpack(ld16<false>(g), gv);
+        Vec<T>::unpack(ld16<false>(g + inter), uv);
 #pragma unroll
         for (int e = 0; e < N; ++e) gv[e] = silu(gv[e]) * uv[e];
-        st16(out + r * inter + (int64_t)j * N, Vec<T>::pack(gv));
+        st16<false>(out + r * inter + (int64_t)j * N, Vec<T>::pack(gv));
     }
 }
 
@@ -136,11 +158,11 @@ __global__ __launch_bounds__(256) void residual_add_kernel(T* __restrict__ res, 
     for (int64_t c = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; c < n_chunks;
          c += (int64_t)gridDim.x * blockDim.x) {
         float a[N], h[N];
-        Vec<T>::unpack(ld16(res + c * N), a);
-        Vec<T>::unpack(ld16(hid + c * N), h);
+        Vec<T>::unpack(ld16<true>(res + c * N), a);
+        Vec<T>::unpack(ld16<true>(hid + c * N), h);
 #pragma unroll
         for (int e = 0; e < N; ++e) a[e] += h[e];
-        st16(res + c * N, Vec<T>::pack(a));
+        st16<true>(res + c * N, Vec<T>::pack(a));
     }
 }
 
