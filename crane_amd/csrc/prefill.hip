@@ -151,8 +151,13 @@ __device__ __forceinline__ bool map_block(int id, int n_qt, int B, int Hkv, int 
     return true;
 }
 
-template <bool CAUSAL, class ROWS>
-__global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(2, 2))) void prefill_bf16_kernel(
+// SPLIT = 2 (a grid too small to fill the chip): 8 waves, two groups of 4 on
+// the same 128 query rows; group g walks its half of the key tiles through its
+// own LDS tiles, and group 1's running (max, sum, O) merge into group 0's
+// through LDS at the end.  Every wave passes the same barriers: a step past a
+// group's half does no copy and no work.
+template <bool CAUSAL, class ROWS, int SPLIT>
+__global__ __launch_bounds__(64 * kWaves * SPLIT) __attribute__((amdgpu_waves_per_eu(2, 2))) void prefill_bf16_kernel(
     const bf16_t* __restrict__ q, const bf16_t* __restrict__ kc, const bf16_t* __restrict__ vc, ROWS rows,
     const int32_t* __restrict__ start_pos, int max_start, int S, int B, int Hq, int Hkv, float scale_log2,
     bf16_t* __restrict__ out) {
@@ -165,18 +170,25 @@ __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(2, 
     const int m0 = qt * kBM;
 
     // K tiles t and t+1 and V tile t are resident while tile t is computed;
-    // K(t+2) and V(t+1) are in flight.
-    __shared__ __attribute__((aligned(1024))) uint8_t kbuf[2][kTileBytes];
-    __shared__ __attribute__((aligned(1024))) uint8_t vbuf[2][kTileBytes];
+    // K(t+2) and V(t+1) are in flight.  One set per group.
+    __shared__ __attribute__((aligned(1024))) uint8_t kbufs[SPLIT][2][kTileBytes];
+    __shared__ __attribute__((aligned(1024))) uint8_t vbufs[SPLIT][2][kTileBytes];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: LDS copy targets are scalar
+    const int wave_all = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: LDS copy targets are scalar
+    const int grp = SPLIT > 1 ? wave_all / kWaves : 0;              // key-range group
+    const int wave = SPLIT > 1 ? wave_all % kWaves : wave_all;      // wave within the group: its query rows
+    auto& kbuf = kbufs[grp];
+    auto& vbuf = vbufs[grp];
     const int n = lane & 31, hh = lane >> 5;
 
     const int L = start + S;                                 // cache rows holding keys for this chunk
     const int kend = CAUSAL ? min(start + m0 + kBM, L) : L;  // keys any row of the tile can see
-    const int n_tiles = (kend + kBN - 1) / kBN;
+    const int n_all = (kend + kBN - 1) / kBN;
+    const int half = (n_all + SPLIT - 1) / SPLIT;            // steps every group takes
+    const int t0 = grp * half;                               // this group's first tile
+    const int n_tiles = max(0, min(half, n_all - t0));       // ... and how many it has
     uint32_t vofs[kCopies];
 #pragma unroll
     for (int i = 0; i < kCopies; ++i) vofs[i] = pinned(copy_voffset(i, wave, lane));
@@ -198,9 +210,11 @@ __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(2, 
             issue_tile(whole, x, wave, vofs, dst);
         }
     };
-    issue(kc, rk, 0, kbuf[0]);
-    issue(vc, rv, 0, vbuf[0]);
-    if (n_tiles > 1) issue(kc, rk, 1, kbuf[1]);
+    if (n_tiles > 0) {
+        issue(kc, rk, t0, kbuf[0]);
+        issue(vc, rv, t0, vbuf[0]);
+    }
+    if (n_tiles > 1) issue(kc, rk, t0 + 1, kbuf[1]);
 
     // Q fragments (B operand of S^T = K Q^T): query row qrow, dims 16ks + 8hh .. +7.
     const int qrow = m0 + wave * 32 + n;
@@ -242,7 +256,8 @@ __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(2, 
             voff[db][h] = pinned(r * 256 + 16 * ((col >> 3) ^ swz(r)) + 2 * (col & 7));
         }
 
-    // Tile 0 is visible to every row (key 0 precedes every query position).
+    // Tile 0 is visible to every row (key 0 precedes every query position);
+    // a later group's first tile need not be (see the -inf guards below).
     if (n_tiles > 1) CRANE_WAIT_VMCNT(2 * kCopies); else CRANE_WAIT_VMCNT(kCopies);  // this wave's K(0) copies
     __syncthreads();                                                   // ... and every wave's
     f32x16_v sa[2], sb[2];
@@ -257,9 +272,10 @@ __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(2, 
         constexpr int par = decltype(parity)::value;
         CRANE_WAIT_VMCNT(0);  // this wave's copies of V(t) and K(t+1) have landed
         __syncthreads();      // ... and every wave's; K(t) and V(t-1) are fully consumed
-        if (t + 2 < n_tiles) issue(kc, rk, t + 2, kbuf[par]);
-        if (t + 1 < n_tiles) issue(vc, rv, t + 1, vbuf[par ^ 1]);
-        const int kt = t * kBN;
+        if (t + 2 < n_tiles) issue(kc, rk, t0 + t + 2, kbuf[par]);
+        if (t + 1 < n_tiles) issue(vc, rv, t0 + t + 1, vbuf[par ^ 1]);
+        if (SPLIT > 1 && t >= n_tiles) return;  // past this group's half: only the barrier
+        const int kt = (t0 + t) * kBN;
         if (CAUSAL && kt > wave_first + 31) return;  // the whole tile is above this wave's diagonal
         if (kt + kBN > kend || (CAUSAL && kt + kBN - 1 > wave_first)) {  // diagonal or last tile
 #pragma unroll
@@ -285,7 +301,9 @@ __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(2, 
         // key 0 is visible to every query, so m_run is finite afterwards).
         if (__any(tmax > m_run + kLazy)) {
             const float m_new = fmaxf(m_run, fmaxf(tmax, __shfl_xor(tmax, 32)));
-            const float alpha = fast_exp2(m_run - m_new);
+            // A later group's row that has seen no key yet keeps m = -inf (and O,
+            // l = 0): its factor must not become exp2(-inf + inf).
+            const float alpha = SPLIT > 1 && m_new == -INFINITY ? 1.f : fast_exp2(m_run - m_new);
             l_run *= alpha;
 #pragma unroll
             for (int i = 0; i < 4; ++i)
@@ -293,7 +311,7 @@ __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(2, 
                 for (int r = 0; r < 16; ++r) oacc[i][r] *= alpha;
             m_run = m_new;
         }
-        const float neg_m = -m_run;
+        const float neg_m = SPLIT > 1 && m_run == -INFINITY ? 0.f : -m_run;  // its p = exp2(-inf) = 0
         float psum = 0.f;
         bf16x8_v pf[4];
 #pragma unroll
@@ -334,9 +352,41 @@ __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(2, 
             }
         }
     };
-    for (int t = 0; t < n_tiles; t += 2) {
+    const int n_steps = SPLIT > 1 ? half : n_tiles;
+    for (int t = 0; t < n_steps; t += 2) {
         step(std::integral_constant<int, 0>{}, t, sa, sb);
-        if (t + 1 < n_tiles) step(std::integral_constant<int, 1>{}, t + 1, sb, sa);
+        if (t + 1 < n_steps) step(std::integral_constant<int, 1>{}, t + 1, sb, sa);
+    }
+
+    if constexpr (SPLIT > 1) {
+        // Group 1's O (in the freed K tiles) and (m, l) (in the freed V tiles)
+        // for each lane, lane-minor; group 0's wave w merges the same query
+        // rows' values.
+        static_assert(SPLIT == 2, "two key groups");
+        static_assert(kWaves * 64 * 64 * 4 <= (int)sizeof(kbufs) && kWaves * 2 * 64 * 4 <= (int)sizeof(vbufs),
+                      "exchange fits the tile space");
+        float* xo = reinterpret_cast<float*>(&kbufs[0][0][0]) + wave * 64 * 64 + lane;
+        float* xml = reinterpret_cast<float*>(&vbufs[0][0][0]) + wave * 2 * 64 + lane;
+        __syncthreads();  // every wave is done with the tiles
+        if (grp == 1) {
+            xml[0] = m_run;
+            xml[64] = l_run;
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) xo[64 * (16 * i + r)] = oacc[i][r];
+        }
+        __syncthreads();
+        if (grp == 1) return;
+        const float m1 = xml[0], l1 = xml[64];
+        const float mm = fmaxf(m_run, m1);
+        const float a0 = m_run == -INFINITY ? 0.f : fast_exp2(m_run - mm);
+        const float a1 = m1 == -INFINITY ? 0.f : fast_exp2(m1 - mm);
+        l_run = l_run * a0 + l1 * a1;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) oacc[i][r] = oacc[i][r] * a0 + xo[64 * (16 * i + r)] * a1;
     }
 
     l_run += __shfl_xor(l_run, 32);  // the two lane halves hold different keys of the row
@@ -388,6 +438,18 @@ __global__ __launch_bounds__(64) void prefill_f32_kernel(const float* __restrict
     *reinterpret_cast<float2*>(op) = make_float2(o0 / l, o1 / l);
 }
 
+// Compute units of the current device (cached per device).
+int device_cus() {
+    static int cus[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (!cus[dev]) {
+        int n = 0;
+        cus[dev] = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0 ? n : 256;
+    }
+    return cus[dev];
+}
+
 // Checks shared by both layouts, then the launch; `rows` addresses the cache.
 template <class ROWS>
 int attn_prefill(const void* q, const void* k_cache, const void* v_cache, const ROWS& rows, const int32_t* start_pos,
@@ -412,14 +474,20 @@ int attn_prefill(const void* q, const void* k_cache, const void* v_cache, const 
         const int64_t chunk = 8LL * n_rep;
         const int64_t blocks = ((units + 7) / 8) * chunk;
         if (blocks > 0x7fffffffLL) return CRANE_HIP_E_INVALID;
-        if (causal)
-            hipLaunchKernelGGL((prefill_bf16_kernel<true, ROWS>), dim3((unsigned)blocks), dim3(64 * kWaves), 0, st,
-                               (const bf16_t*)q, (const bf16_t*)k_cache, (const bf16_t*)v_cache, rows, start_pos,
-                               (int)max_start, S, B, Hq, Hkv, sl, (bf16_t*)out);
-        else
-            hipLaunchKernelGGL((prefill_bf16_kernel<false, ROWS>), dim3((unsigned)blocks), dim3(64 * kWaves), 0, st,
-                               (const bf16_t*)q, (const bf16_t*)k_cache, (const bf16_t*)v_cache, rows, start_pos,
-                               (int)max_start, S, B, Hq, Hkv, sl, (bf16_t*)out);
+        // A grid of at most one workgroup per CU leaves each SIMD one wave and the
+        // last query tiles' key walk as the critical path: split the keys of
+        // each tile between two groups of waves instead.
+        const bool split = blocks <= (int64_t)device_cus();
+#define CRANE_PREFILL_LAUNCH(C, SP)                                                                              \
+    hipLaunchKernelGGL((prefill_bf16_kernel<C, ROWS, SP>), dim3((unsigned)blocks), dim3(64 * kWaves * SP), 0, st, \
+                       (const bf16_t*)q, (const bf16_t*)k_cache, (const bf16_t*)v_cache, rows, start_pos,        \
+                       (int)max_start, S, B, Hq, Hkv, sl, (bf16_t*)out)
+        if (causal) {
+            if (split) CRANE_PREFILL_LAUNCH(true, 2); else CRANE_PREFILL_LAUNCH(true, 1);
+        } else {
+            if (split) CRANE_PREFILL_LAUNCH(false, 2); else CRANE_PREFILL_LAUNCH(false, 1);
+        }
+#undef CRANE_PREFILL_LAUNCH
     } else {
         const float sl = scale * kLog2e;
         const dim3 grid((unsigned)S, (unsigned)Hq, (unsigned)B);
