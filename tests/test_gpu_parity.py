@@ -266,17 +266,35 @@ def test_prefill_last_row_equals_decode(gpu):
 
 
 def test_decode_workspace_reuse_across_shapes(gpu, orc):
-    """One workspace serves successive calls of different shapes."""
+    """One workspace serves successive calls of different shapes, including
+    calls with more (sequence, head) rows than an earlier one and a long call
+    repeated after shorter ones: no call depends on what an earlier one left."""
     from crane_amd import ops
     ws = torch.zeros(ops.decode_workspace_bytes(8, 32, 8, 3000) + 4096, dtype=torch.uint8, device=gpu)
     for i, (B, Hq, Hkv, lens) in enumerate([(8, 32, 8, [3000, 1, 700, 2999, 256, 257, 1024, 77]),
-                                             (3, 8, 2, [5, 600, 2048]), (8, 32, 8, [100] * 8)]):
+                                             (3, 8, 2, [5, 600, 2048]), (8, 32, 8, [100] * 8),
+                                             (24, 16, 8, [300 + 13 * j for j in range(24)]),
+                                             (8, 32, 8, [3000, 1, 700, 2999, 256, 257, 1024, 77])]):
         note(f"workspace reuse call {i}: B={B} lens={lens}")
         q, k, v, lens = cases.decode_case(400 + i, B, Hq, Hkv, lens, dtype="bf16")
         out = host(ops.attention_decode(dev_t(q, "bf16", gpu), dev_t(k, "bf16", gpu), dev_t(v, "bf16", gpu),
                                         i32(lens, gpu), int(lens.max()), workspace=ws)).reshape(B, Hq * D)
         ref = orc.attn_decode(q, k, v, lens, cases.scale(), "bf16")
         assert_close(out, ref, "bf16", f"reuse call {i}")
+
+
+def test_decode_64_heads_per_kv_head(gpu, orc):
+    """64 q heads on one kv head (eight 8-head groups share each K/V row) over
+    1025 ragged sequences, 65600 (sequence, head) rows in all."""
+    from crane_amd import ops
+    B, Hq, Hkv = 1025, 64, 1
+    lens = cases.rng(57).integers(0, 520, size=B).astype(np.int32)
+    note(f"decode 64 heads per kv head: B={B} Hq={Hq} Hkv={Hkv} max_len={lens.max()}")
+    q, k, v, lens = cases.decode_case(58, B, Hq, Hkv, lens, dtype="bf16")
+    out = host(ops.attention_decode(dev_t(q, "bf16", gpu), dev_t(k, "bf16", gpu), dev_t(v, "bf16", gpu),
+                                    i32(lens, gpu), int(lens.max()))).reshape(B, Hq * D)
+    ref = orc.attn_decode(q, k, v, lens, cases.scale(), "bf16")
+    assert_close(out, ref, "bf16", "64 heads per kv head")
 
 
 def test_decode_large_batch(gpu, orc):
