@@ -57,8 +57,11 @@ class Gemm {
         return CRANE_HIP_OK;
     }
 
+    // Serialised per context: the plan map, and the bias pointer set on a
+    // shared descriptor just before the call that reads it.
     int linear(const void* x, const void* w, const void* bias, void* y, int64_t M, int64_t N, int64_t K, int dtype,
                hipStream_t st) {
+        std::lock_guard<std::mutex> lock(mu_);
         Plan* p = nullptr;
         int rc = plan(M, N, K, dtype, bias != nullptr, &p);
         if (rc) return rc;
@@ -119,6 +122,7 @@ class Gemm {
         return CRANE_HIP_OK;
     }
 
+    std::mutex mu_;
     hipblasLtHandle_t handle_ = nullptr;
     void* ws_ = nullptr;
     size_t ws_bytes_ = 0;

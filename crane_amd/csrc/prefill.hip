@@ -37,6 +37,7 @@
 // f32 kernel: a plain wave-per-query-row online-softmax kernel; Crane serves
 // prefill in bf16 on GPU (crane-serve/src/lib.rs:123-150), f32 is kept for
 // completeness of the operator.
+#include <atomic>
 #include <type_traits>
 
 #include "common.h"
@@ -438,16 +439,19 @@ __global__ __launch_bounds__(64) void prefill_f32_kernel(const float* __restrict
     *reinterpret_cast<float2*>(op) = make_float2(o0 / l, o1 / l);
 }
 
-// Compute units of the current device (cached per device).
+// Compute units of the current device (cached per device; host threads may
+// race to fill an entry, with the same value).
 int device_cus() {
-    static int cus[64] = {0};
+    static std::atomic<int> cus[64];
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-    if (!cus[dev]) {
-        int n = 0;
-        cus[dev] = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0 ? n : 256;
+    int n = cus[dev].load(std::memory_order_relaxed);
+    if (!n) {
+        n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+        cus[dev].store(n, std::memory_order_relaxed);
     }
-    return cus[dev];
+    return n;
 }
 
 // Checks shared by both layouts, then the launch; `rows` addresses the cache.

@@ -462,7 +462,9 @@ def residual_add(residual: torch.Tensor, hidden: torch.Tensor) -> torch.Tensor:
 # qkv_proj whose output rows feed qk_norm_rope_append, and o_proj.
 
 class _GemmContext:
-    """One crane_gemm (hipBLASLt handle, workspace, per-shape plans) per device."""
+    """One crane_gemm (hipBLASLt handle, workspace, per-shape plans) per
+    (device, stream): calls on one stream are ordered, so they can share its
+    workspace; calls on different streams may overlap and must not."""
 
     def __init__(self, device: torch.device):
         h = ctypes.c_void_p()
@@ -481,9 +483,10 @@ _GEMMS: dict = {}
 
 
 def _gemm(device: torch.device) -> _GemmContext:
-    ctx = _GEMMS.get(device)
+    key = (device, torch.cuda.current_stream(device).cuda_stream)
+    ctx = _GEMMS.get(key)
     if ctx is None:
-        ctx = _GEMMS[device] = _GemmContext(device)
+        ctx = _GEMMS[key] = _GemmContext(device)
     return ctx
 
 

@@ -15,9 +15,11 @@
  * product and then the sum).  A crane_gemm context holds the hipBLASLt handle,
  * a workspace allocated at creation and the algorithm chosen for each shape
  * (the heuristic query runs once per shape).  Conventions otherwise as in
- * crane_hip.h; crane_gemm_linear does not allocate or synchronise.  One
- * context must not be used from two threads at once; it belongs to the device
- * that was current at creation.
+ * crane_hip.h; crane_gemm_linear does not allocate or synchronise.  Calls on
+ * one context from several threads are serialised on the host.  Every call
+ * on a context uses its one workspace, so calls whose GPU work may overlap
+ * (on different streams) need different contexts.  A context belongs to the
+ * device that was current at creation.
  */
 #ifndef CRANE_GEMM_H
 #define CRANE_GEMM_H

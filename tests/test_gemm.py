@@ -128,3 +128,62 @@ def test_qkv_proj_feeds_the_append(gpu, orc):
     assert_ulp_close(q.float().cpu().numpy(), q_ref, "bf16", "q after the append", min_exact=0.999)
     assert_ulp_close(kc.float().cpu().numpy(), kref, "bf16", "k cache after the append", min_exact=0.999)
     np.testing.assert_array_equal(vc.float().cpu().numpy(), vref)
+
+
+@pytest.mark.gpu
+def test_linear_on_two_streams_and_threads(gpu, orc):
+    """Each stream gets its own context (its own workspace), so projections on
+    two streams may overlap; host threads calling into one context at once,
+    while new shapes are being planned, are serialised.  Every result is
+    bit-identical to the same product on the default stream."""
+    import threading
+    import torch
+    from crane_amd import ops
+    shapes = [(64 + 7 * i, 256 + 32 * i, 512) for i in range(6)]
+    xs, ws, refs = [], [], []
+    for i, (M, N, K) in enumerate(shapes):
+        x, w, _ = _case(700 + i, M, N, K, "bf16", False)
+        xs.append(_t(x, "bf16", gpu))
+        ws.append(_t(w, "bf16", gpu))
+    torch.cuda.synchronize()
+    refs = [ops.linear(x, w) for x, w in zip(xs, ws)]
+    torch.cuda.synchronize()
+    print("linear: two streams", flush=True)
+    s1, s2 = torch.cuda.Stream(device=gpu), torch.cuda.Stream(device=gpu)
+    outs = {}
+    for s in (s1, s2):
+        s.wait_stream(torch.cuda.current_stream(gpu))
+    with torch.cuda.stream(s1):
+        outs[1] = [ops.linear(x, w) for x, w in zip(xs, ws)]
+    with torch.cuda.stream(s2):
+        outs[2] = [ops.linear(x, w) for x, w in reversed(list(zip(xs, ws)))][::-1]
+    torch.cuda.synchronize()
+    assert ops._gemm(gpu) is not None and len({k for k in ops._GEMMS if k[0] == gpu}) >= 3
+    for k in (1, 2):
+        for got, ref in zip(outs[k], refs):
+            assert torch.equal(got, ref), "a side stream's product differs"
+    print("linear: four host threads on one stream", flush=True)
+    results, errors = {}, []
+
+    def worker(j):
+        try:
+            new = [(40 + 3 * j + i, 192 + 64 * j, 256) for i in range(3)]  # shapes no one planned yet
+            got = []
+            for (M, N, K) in new:
+                x, w, _ = _case(800 + 10 * j + M, M, N, K, "bf16", False)
+                xt, wt = _t(x, "bf16", gpu), _t(w, "bf16", gpu)
+                got.append((ops.linear(xt, wt), xt, wt))
+            results[j] = got
+        except Exception as e:  # reported below, in the test's thread
+            errors.append(repr(e))
+
+    threads = [threading.Thread(target=worker, args=(j,)) for j in range(4)]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join()
+    torch.cuda.synchronize()
+    assert not errors, errors
+    for j, got in results.items():
+        for y, xt, wt in got:
+            assert torch.equal(y, ops.linear(xt, wt)), f"thread {j}: product differs on a second call"
