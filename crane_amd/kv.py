@@ -18,7 +18,7 @@ import torch
 
 from . import _lib
 from ._lib import CraneHipError, check
-from .ops import HEAD_DIM, _ORDERS, _dtype_code, _ptr, _stream
+from .ops import HEAD_DIM, _ORDERS, _dev, _dtype_code, _ptr, _rope_inputs, _stream
 
 _DT = {torch.float32: _lib.F32, torch.bfloat16: _lib.BF16}
 
@@ -27,6 +27,30 @@ def grown_capacity(cap: int, needed: int) -> int:
     """Rows a cache of `cap` rows holds after making room for `needed` rows
     (Crane's policy: unchanged if it fits, else needed + 256)."""
     return int(_lib.lib().crane_kv_grown_capacity(cap, needed))
+
+
+def _check_q(q: torch.Tensor, ndim: int, batch: int, dtype: torch.dtype, device: torch.device) -> None:
+    """q for a cache's attention ops: [B, Hq, D] (decode) or [B, Hq, S, D]
+    (prefill) in the cache's dtype and on its device; the library reads it
+    with the cache's element size."""
+    if _dev(q) != device:
+        raise CraneHipError(_lib.E_INVALID, f"q on {q.device}, cache on {device}")
+    if q.dtype != dtype:
+        raise CraneHipError(_lib.E_DTYPE, f"q dtype {q.dtype} != cache dtype {dtype}")
+    if q.dim() != ndim or q.shape[0] != batch or q.shape[-1] != HEAD_DIM:
+        shape = "[B, Hq, D]" if ndim == 3 else "[B, Hq, S, D]"
+        raise CraneHipError(_lib.E_INVALID, f"q must be {shape} for a batch of {batch}, D = {HEAD_DIM}")
+
+
+def _check_append(qkv: torch.Tensor, cos, sin, positions, num_heads: int, num_kv_heads: int, q_norm_w, k_norm_w,
+                  order: str, batch: int, dtype: torch.dtype, device: torch.device) -> None:
+    _rope_inputs(qkv, (num_heads + 2 * num_kv_heads) * HEAD_DIM, cos, sin, positions, q_norm_w, k_norm_w, order)
+    if qkv.device != device:
+        raise CraneHipError(_lib.E_INVALID, f"qkv on {qkv.device}, cache on {device}")
+    if qkv.shape[0] != batch:
+        raise CraneHipError(_lib.E_INVALID, f"qkv batch {qkv.shape[0]} != {batch}")
+    if qkv.dtype != dtype:
+        raise CraneHipError(_lib.E_DTYPE, f"qkv dtype {qkv.dtype} != cache dtype {dtype}")
 
 
 class _DeviceView:
@@ -133,12 +157,8 @@ class KvCache:
                    eps: float = 1e-6, order: str = "norm_then_rope") -> torch.Tensor:
         """Fused QK-norm + RoPE written into this cache at the current lengths
         (growing it as update_kv_cache would); returns q [B, Hq, S, D]."""
-        if qkv.dim() != 3 or qkv.shape[0] != self.batch:
-            raise CraneHipError(_lib.E_INVALID, "qkv must be [B, S, (Hq+2Hkv)*D]")
-        if qkv.dtype != self.dtype:
-            raise CraneHipError(_lib.E_DTYPE, f"qkv dtype {qkv.dtype} != cache dtype {self.dtype}")
-        if order not in _ORDERS:
-            raise CraneHipError(_lib.E_INVALID, f"order {order!r}")
+        _check_append(qkv, cos, sin, positions, num_heads, self.num_kv_heads, q_norm_w, k_norm_w, order,
+                      self.batch, self.dtype, self.device)
         B, S, _ = qkv.shape
         q_out = torch.empty((B, num_heads, S, HEAD_DIM), dtype=qkv.dtype, device=qkv.device)
         check(_lib.lib().crane_kv_append_qkv(
@@ -151,9 +171,13 @@ class KvCache:
                workspace: Optional[torch.Tensor] = None) -> torch.Tensor:
         """Decode attention of q [B, Hq, D] over every sequence's rows; [B, 1, Hq*D]."""
         from .ops import decode_workspace
+        _check_q(q, 3, self.batch, self.dtype, self.device)
+        q = q.contiguous()
         B, Hq, D = q.shape
         max_kv = max(self.lengths)
         need = _lib.lib().crane_hip_attn_decode_workspace(B, Hq, self.num_kv_heads, D, max_kv, _dtype_code(q))
+        if workspace is not None:
+            _dev(q, workspace)
         ws = workspace if workspace is not None else decode_workspace(q.device, need)
         out = torch.empty((B, 1, Hq * D), dtype=q.dtype, device=q.device)
         check(_lib.lib().crane_kv_decode(self._h, q.data_ptr(), Hq, scale if scale else D ** -0.5, ws.data_ptr(),
@@ -164,6 +188,7 @@ class KvCache:
     def prefill(self, q: torch.Tensor, scale: Optional[float] = None, causal: bool = True) -> torch.Tensor:
         """Attention of q [B, Hq, S, D] (the last S rows of every sequence) over
         the cache; [B, S, Hq*D]."""
+        _check_q(q, 4, self.batch, self.dtype, self.device)
         B, Hq, S, D = q.shape
         out = torch.empty((B, S, Hq * D), dtype=q.dtype, device=q.device)
         check(_lib.lib().crane_kv_prefill(self._h, q.contiguous().data_ptr(), Hq, S, scale if scale else D ** -0.5,
@@ -297,12 +322,8 @@ class PagedKvCache:
                    num_heads: int, q_norm_w: Optional[torch.Tensor] = None, k_norm_w: Optional[torch.Tensor] = None,
                    eps: float = 1e-6, order: str = "norm_then_rope") -> torch.Tensor:
         """Fused QK-norm + RoPE written at the batch sequences' lengths; q [B, Hq, S, D]."""
-        if qkv.dim() != 3 or qkv.shape[0] != len(self._batch):
-            raise CraneHipError(_lib.E_INVALID, "qkv must be [B, S, (Hq+2Hkv)*D] for the batch")
-        if qkv.dtype != self.dtype:
-            raise CraneHipError(_lib.E_DTYPE, f"qkv dtype {qkv.dtype} != cache dtype {self.dtype}")
-        if order not in _ORDERS:
-            raise CraneHipError(_lib.E_INVALID, f"order {order!r}")
+        _check_append(qkv, cos, sin, positions, num_heads, self.num_kv_heads, q_norm_w, k_norm_w, order,
+                      len(self._batch), self.dtype, self.device)
         B, S, _ = qkv.shape
         q_out = torch.empty((B, num_heads, S, HEAD_DIM), dtype=qkv.dtype, device=qkv.device)
         check(_lib.lib().crane_pkv_append_qkv(
@@ -315,9 +336,13 @@ class PagedKvCache:
                workspace: Optional[torch.Tensor] = None) -> torch.Tensor:
         """Decode attention of q [B, Hq, D] over the batch's rows; [B, 1, Hq*D]."""
         from .ops import decode_workspace
+        _check_q(q, 3, len(self._batch), self.dtype, self.device)
+        q = q.contiguous()
         B, Hq, D = q.shape
         need = _lib.lib().crane_hip_attn_decode_workspace(B, Hq, self.num_kv_heads, D, max(self.lengths),
                                                           _dtype_code(q))
+        if workspace is not None:
+            _dev(q, workspace)
         ws = workspace if workspace is not None else decode_workspace(q.device, need)
         out = torch.empty((B, 1, Hq * D), dtype=q.dtype, device=q.device)
         check(_lib.lib().crane_pkv_decode(self._h, q.data_ptr(), Hq, scale if scale else D ** -0.5, ws.data_ptr(),
@@ -328,6 +353,7 @@ class PagedKvCache:
     def prefill(self, q: torch.Tensor, scale: Optional[float] = None, causal: bool = True) -> torch.Tensor:
         """Attention of q [B, Hq, S, D] (the last S rows of every batch
         sequence) over its rows; [B, S, Hq*D]."""
+        _check_q(q, 4, len(self._batch), self.dtype, self.device)
         B, Hq, S, D = q.shape
         out = torch.empty((B, S, Hq * D), dtype=q.dtype, device=q.device)
         check(_lib.lib().crane_pkv_prefill(self._h, q.contiguous().data_ptr(), Hq, S, scale if scale else D ** -0.5,

@@ -103,6 +103,37 @@ def rope_tables_qwen2(head_dim: int, theta: float, max_pos: int, device: torch.d
 
 # ------------------------------------------------------------ fused append op
 
+def _rope_inputs(x: torch.Tensor, width: int, cos: torch.Tensor, sin: torch.Tensor, positions: torch.Tensor,
+                 q_norm_w: Optional[torch.Tensor], k_norm_w: Optional[torch.Tensor], order: str, name: str = "qkv"):
+    """Checks shared by every fused-rope entry point, for rows x [B, S, width]
+    (the kernels read `width` elements of each row and cos/sin rows up to
+    positions[b] + S - 1, bounds-checked against the table): returns (device,
+    B, S)."""
+    dev = _dev(x, cos, sin, positions, q_norm_w, k_norm_w)
+    if x.dim() != 3:
+        raise CraneHipError(_lib.E_INVALID, f"{name} must be [B, S, {width}]")
+    B, S, W = x.shape
+    if W != width:
+        raise CraneHipError(_lib.E_INVALID, f"{name} last dim {W} != {width}")
+    _dtype_code(x)
+    for t, n in ((cos, "cos"), (sin, "sin"), (q_norm_w, "q_norm_w"), (k_norm_w, "k_norm_w")):
+        if t is not None and t.dtype != x.dtype:
+            raise CraneHipError(_lib.E_DTYPE, f"{n} dtype {t.dtype} != {name} dtype {x.dtype}")
+    for t, n in ((q_norm_w, "q_norm_w"), (k_norm_w, "k_norm_w")):
+        if t is not None and (t.numel() != HEAD_DIM or not t.is_contiguous()):
+            raise CraneHipError(_lib.E_INVALID, f"{n} must be a contiguous [{HEAD_DIM}] weight")
+    if x.stride(2) != 1 or x.stride(0) != S * x.stride(1):
+        raise CraneHipError(_lib.E_INVALID, f"{name} rows must be dense with a unit inner stride")
+    _contig(cos, "cos")
+    _contig(sin, "sin")
+    if cos.shape != sin.shape or cos.dim() != 2 or cos.shape[1] != HEAD_DIM // 2:
+        raise CraneHipError(_lib.E_INVALID, "cos/sin must be [max_pos, D/2]")
+    _i32(positions, B, "positions")
+    if order not in _ORDERS:
+        raise CraneHipError(_lib.E_INVALID, f"order {order!r}")
+    return dev, B, S
+
+
 def qk_norm_rope_append(qkv: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,
                         positions: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
                         cache_len: torch.Tensor, max_rows: int, num_heads: int, num_kv_heads: int,
@@ -116,31 +147,18 @@ def qk_norm_rope_append(qkv: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,
     order "rope_then_norm" is Hunyuan's (hunyuan_dense/modeling.rs:541-555) and
     "rope_only" Qwen2.5's (qwen2.rs:75-76).  `max_rows` is a host-side bound
     on cache_len[b] + S, checked against the cache capacity."""
-    dev = _dev(qkv, cos, sin, positions, k_cache, v_cache, cache_len, q_norm_w, k_norm_w)
-    if qkv.dim() != 3:
-        raise CraneHipError(_lib.E_INVALID, "qkv must be [B, S, (Hq+2Hkv)*D]")
-    B, S, W = qkv.shape
     D = HEAD_DIM
-    if W != (num_heads + 2 * num_kv_heads) * D:
-        raise CraneHipError(_lib.E_INVALID, f"qkv last dim {W} != (Hq+2Hkv)*{D}")
+    dev, B, S = _rope_inputs(qkv, (num_heads + 2 * num_kv_heads) * D, cos, sin, positions, q_norm_w, k_norm_w, order)
+    _dev(qkv, k_cache, v_cache, cache_len)
     if k_cache.shape != v_cache.shape or k_cache.dim() != 4 or k_cache.shape[0] != B or \
             k_cache.shape[1] != num_kv_heads or k_cache.shape[3] != D:
         raise CraneHipError(_lib.E_INVALID, "caches must be [B, Hkv, cap, D]")
     dt = _dtype_code(qkv)
-    for t, name in ((cos, "cos"), (sin, "sin"), (k_cache, "k_cache"), (v_cache, "v_cache"),
-                    (q_norm_w, "q_norm_w"), (k_norm_w, "k_norm_w")):
-        if t is not None and t.dtype != qkv.dtype:
+    for t, name in ((k_cache, "k_cache"), (v_cache, "v_cache")):
+        if t.dtype != qkv.dtype:
             raise CraneHipError(_lib.E_DTYPE, f"{name} dtype {t.dtype} != qkv dtype {qkv.dtype}")
-    if qkv.stride(2) != 1 or qkv.stride(0) != S * qkv.stride(1):
-        raise CraneHipError(_lib.E_INVALID, "qkv rows must be dense with a unit inner stride")
-    for t, name in ((cos, "cos"), (sin, "sin"), (k_cache, "k_cache"), (v_cache, "v_cache")):
         _contig(t, name)
-    if cos.shape != sin.shape or cos.dim() != 2 or cos.shape[1] != D // 2:
-        raise CraneHipError(_lib.E_INVALID, "cos/sin must be [max_pos, D/2]")
-    _i32(positions, B, "positions")
     _i32(cache_len, B, "cache_len")
-    if order not in _ORDERS:
-        raise CraneHipError(_lib.E_INVALID, f"order {order!r}")
     q_out = torch.empty((B, num_heads, S, D), dtype=qkv.dtype, device=dev)
     rc = _lib.lib().crane_hip_qknorm_rope_append(
         qkv.data_ptr(), qkv.stride(1), _ptr(q_norm_w), _ptr(k_norm_w), eps, _ORDERS[order],
@@ -159,26 +177,9 @@ def q_norm_rope(q: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, positions
     then query_layernorm.  q is [B, S, Hq*D] (rows may be a narrowed view with
     a unit inner stride); returns [B, Hq, S, D] for the attention ops, which
     then read the anchor layer's cache."""
-    dev = _dev(q, cos, sin, positions, q_norm_w)
-    if q.dim() != 3:
-        raise CraneHipError(_lib.E_INVALID, "q must be [B, S, Hq*D]")
-    B, S, W = q.shape
     D = HEAD_DIM
-    if W != num_heads * D:
-        raise CraneHipError(_lib.E_INVALID, f"q last dim {W} != Hq*{D}")
+    dev, B, S = _rope_inputs(q, num_heads * D, cos, sin, positions, q_norm_w, None, order, name="q")
     dt = _dtype_code(q)
-    for t, name in ((cos, "cos"), (sin, "sin"), (q_norm_w, "q_norm_w")):
-        if t is not None and t.dtype != q.dtype:
-            raise CraneHipError(_lib.E_DTYPE, f"{name} dtype {t.dtype} != q dtype {q.dtype}")
-    if q.stride(2) != 1 or q.stride(0) != S * q.stride(1):
-        raise CraneHipError(_lib.E_INVALID, "q rows must be dense with a unit inner stride")
-    _contig(cos, "cos")
-    _contig(sin, "sin")
-    if cos.shape != sin.shape or cos.dim() != 2 or cos.shape[1] != D // 2:
-        raise CraneHipError(_lib.E_INVALID, "cos/sin must be [max_pos, D/2]")
-    _i32(positions, B, "positions")
-    if order not in _ORDERS:
-        raise CraneHipError(_lib.E_INVALID, f"order {order!r}")
     q_out = torch.empty((B, num_heads, S, D), dtype=q.dtype, device=dev)
     rc = _lib.lib().crane_hip_qnorm_rope(
         q.data_ptr(), q.stride(1), _ptr(q_norm_w), eps, _ORDERS[order], cos.data_ptr(), sin.data_ptr(),
@@ -309,27 +310,13 @@ def qk_norm_rope_append_paged(qkv: torch.Tensor, cos: torch.Tensor, sin: torch.T
                               order: str = "norm_then_rope") -> torch.Tensor:
     """qk_norm_rope_append into a paged cache: token s of sequence b lands in
     its row cache_len[b]+s.  Returns q [B, Hq, S, D]."""
-    dev = _dev(qkv, cos, sin, positions, k_pool, v_pool, block_table, cache_len, q_norm_w, k_norm_w)
+    _dev(qkv, k_pool, v_pool, block_table, cache_len)
     if qkv.dim() != 3:
         raise CraneHipError(_lib.E_INVALID, "qkv must be [B, S, (Hq+2Hkv)*D]")
-    B, S, W = qkv.shape
-    n_pages, Hkv, page_rows, stride = _paged_args(k_pool, v_pool, block_table, B, qkv.dtype)
-    if W != (num_heads + 2 * Hkv) * HEAD_DIM:
-        raise CraneHipError(_lib.E_INVALID, f"qkv last dim {W} != (Hq+2Hkv)*{HEAD_DIM}")
+    n_pages, Hkv, page_rows, stride = _paged_args(k_pool, v_pool, block_table, qkv.shape[0], qkv.dtype)
+    dev, B, S = _rope_inputs(qkv, (num_heads + 2 * Hkv) * HEAD_DIM, cos, sin, positions, q_norm_w, k_norm_w, order)
     dt = _dtype_code(qkv)
-    for t, name in ((cos, "cos"), (sin, "sin"), (q_norm_w, "q_norm_w"), (k_norm_w, "k_norm_w")):
-        if t is not None and t.dtype != qkv.dtype:
-            raise CraneHipError(_lib.E_DTYPE, f"{name} dtype {t.dtype} != qkv dtype {qkv.dtype}")
-    if qkv.stride(2) != 1 or qkv.stride(0) != S * qkv.stride(1):
-        raise CraneHipError(_lib.E_INVALID, "qkv rows must be dense with a unit inner stride")
-    _contig(cos, "cos")
-    _contig(sin, "sin")
-    if cos.shape != sin.shape or cos.dim() != 2 or cos.shape[1] != HEAD_DIM // 2:
-        raise CraneHipError(_lib.E_INVALID, "cos/sin must be [max_pos, D/2]")
-    _i32(positions, B, "positions")
     _i32(cache_len, B, "cache_len")
-    if order not in _ORDERS:
-        raise CraneHipError(_lib.E_INVALID, f"order {order!r}")
     q_out = torch.empty((B, num_heads, S, HEAD_DIM), dtype=qkv.dtype, device=dev)
     rc = _lib.lib().crane_hip_qknorm_rope_append_paged(
         qkv.data_ptr(), qkv.stride(1), _ptr(q_norm_w), _ptr(k_norm_w), eps, _ORDERS[order], cos.data_ptr(),
