@@ -477,6 +477,19 @@ def _gemm(device: torch.device) -> _GemmContext:
     return ctx
 
 
+def release_stream(device: Optional[torch.device] = None, stream: Optional[torch.cuda.Stream] = None) -> None:
+    """Drop the decode workspace and the GEMM context kept for `stream`
+    (default: the current stream of `device`).  Both live as long as their
+    stream is in use, one per (device, stream); a caller that retires a stream
+    releases them here.  The GEMM context's destruction frees its workspace
+    with hipFree, which waits for work already queued on the device."""
+    dev = torch.device(device) if device is not None else torch.device("cuda", torch.cuda.current_device())
+    st = stream if stream is not None else torch.cuda.current_stream(dev)
+    key = (dev, st.cuda_stream)
+    _WORKSPACES.pop(key, None)
+    _GEMMS.pop(key, None)
+
+
 def linear(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor] = None) -> torch.Tensor:
     """candle Linear::forward: x [..., K] with weight [N, K] (and bias [N]) ->
     [..., N]; f32 accumulation, the bias added in the GEMM epilogue."""

@@ -162,6 +162,10 @@ def test_linear_on_two_streams_and_threads(gpu, orc):
     for k in (1, 2):
         for got, ref in zip(outs[k], refs):
             assert torch.equal(got, ref), "a side stream's product differs"
+    for st in (s1, s2):  # retire the side streams' contexts
+        ops.release_stream(gpu, st)
+        assert (gpu, st.cuda_stream) not in ops._GEMMS
+    assert torch.equal(ops.linear(xs[0], ws[0]), refs[0])  # the default stream's context is untouched
     print("linear: four host threads on one stream", flush=True)
     results, errors = {}, []
 
