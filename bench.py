@@ -553,7 +553,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: the attention path runs on a single MI355X and this build "
-              "launches nothing on a second GPU (see the sharding notes in DESIGN.md). Use --gpus 1.",
+              "launches nothing on a second GPU (the kernels would shard by kv head across GPUs). Use --gpus 1.",
               file=sys.stderr)
         sys.exit(2)
 

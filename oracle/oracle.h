@@ -63,7 +63,7 @@ void orc_rope_tables_qwen2(int dim, double theta, int max_pos, int dtype, float*
  * ops::rms_norm path (true for a contiguous input) or the LayerNorm fallback. */
 void orc_rms_norm(const float* x, float* y, size_t rows, int d, const float* w, float eps,
                   int contiguous, int dtype);
-/* Layer rows.  Crane's fused SiLU(gate) * up over
+/* The decoder layer's row ops.  Crane's fused SiLU(gate) * up over
  * gate_up [rows, 2*inter] (gate || up): f64 = 0 is the f32 formula of its CUDA
  * kernel, f64 = 1 its cpu_fwd (f64, one conversion to T). */
 void orc_silu_mul(const float* gate_up, float* out, size_t rows, int inter, int f64, int dtype);
