@@ -30,7 +30,9 @@
 //      (v_j, v_j+1) per dim.  The 4 row groups of a wave are summed with lane
 //      permutes and the 4 waves through LDS.
 // A sequence that fits one chunk is normalised and written directly; longer
-// ones leave their unnormalised f32 partial and (m, l) in the workspace.
+// ones leave a partial row and its (m, l) in the workspace: for bf16 the row
+// normalised by the chunk's sum l and stored in bf16 (half the bytes the
+// merge reads; sums stay in f32), for f32 the unnormalised f32 row.
 // Kernel 2 (decode_merge_kernel): the log-sum-exp merge of those partials.
 //
 // Crane's grouped decode pre-scales q in the model dtype (candle affine with
@@ -323,6 +325,9 @@ __device__ __forceinline__ void decode_item(
         const float v = red[0][h][d] + red[1][h][d] + red[2][h][d] + red[3][h][d];
         if (n_chunks == 1)  // the whole sequence fits one chunk: normalise and finish here
             Elem<T>::store(out + ((int64_t)b * Hq + h0 + h) * kHeadDim + d, v / ml[h][1]);
+        else if constexpr (kBf16)  // bf16 partials are stored normalised by the chunk's sum (merge weight w l)
+            reinterpret_cast<bf16_t*>(ws_o)[(((int64_t)b * Hq + h0 + h) * nsplit + c) * kHeadDim + d] =
+                f32_to_bf16(v / ml[h][1]);
         else
             ws_o[(((int64_t)b * Hq + h0 + h) * nsplit + c) * kHeadDim + d] = v;
     }
@@ -350,77 +355,100 @@ __global__ __launch_bounds__(kThreads) void decode_chunk_kernel(
                                 out);
 }
 
-// Kernel 2: log-sum-exp merge of one (sequence, q head)'s partials.  Thread
-// (p, d) owns output dim d for splits p, p + P, p + 2P, ...  After kv_len,
-// every load is issued at once: each thread loads its first kMergeRegs
-// partials into registers while the block reduces the (m, l) pairs, so up to
-// P * kMergeRegs splits cost one memory round trip.  P = 1 covers up to 16
-// splits; more use P = 4, whose partition sums meet in LDS.
+// Kernel 2: log-sum-exp merge of one (sequence, q head)'s partials.  Wave p
+// is partition p: its lane l owns output dims 2l and 2l+1 for splits p,
+// p + P, p + 2P, ... (one 4-byte load per split for bf16 partials, 8 bytes
+// for f32).  After kv_len, every load is issued at once: each lane loads its
+// first kMergeRegs partials into registers while the block reduces the
+// (m, l) pairs, so up to P * kMergeRegs splits cost one memory round trip.
+// The P partition sums meet in LDS.  Used for more than kMergeRegs splits.
 constexpr int kMergeRegs = 16;
 template <typename T, int CH, int P>
-__global__ __launch_bounds__(kHeadDim * P) void decode_merge_kernel(
+__global__ __launch_bounds__(64 * P) void decode_merge_kernel(
     const float* __restrict__ ws_o, const float* __restrict__ ws_ml, const int32_t* __restrict__ kv_len,
     int max_kv, int Hq, int n_rep, int nsplit, T* __restrict__ out) {
-    constexpr int kWaves = kHeadDim * P / 64;
+    constexpr bool kBf16 = std::is_same<T, bf16_t>::value;
     __shared__ float w_lds[kMaxSplits];
-    __shared__ float red[kWaves];
-    __shared__ float part[P > 1 ? P - 1 : 1][kHeadDim];
+    __shared__ float red[P];
+    __shared__ float2 part[P - 1][kHeadDim / 2];
     // grid (groups, B, G), the chunk kernel's (groups, B) with the group's G
     // heads last: workgroup ids then fall on the XCD that ran the head's
     // chunks (measured 0.5% at config 3, 1% at config 5).
     const int G = (int)gridDim.z, sub = n_rep / G, gi = (int)blockIdx.x, b = (int)blockIdx.y;
     const int bh = b * Hq + (gi / sub) * n_rep + (gi % sub) * G + (int)blockIdx.z;
     const int tid = threadIdx.x;
-    const int d = tid % kHeadDim, p = tid / kHeadDim;
+    const int lane = tid & 63, p = tid >> 6;
     const int L = min(kv_len[b], max_kv);
     const int nc = (L + CH - 1) / CH;
     if (nc <= 1) return;  // written by the split kernel
     const float* pm = ws_ml + (int64_t)bh * nsplit * 2;
-    const float* po = ws_o + (int64_t)bh * nsplit * kHeadDim + d;
-    float x[kMergeRegs];
+    const float2* po = reinterpret_cast<const float2*>(ws_o + (int64_t)bh * nsplit * kHeadDim) + lane;
+    const uint32_t* pob = reinterpret_cast<const uint32_t*>(reinterpret_cast<const bf16_t*>(ws_o) +
+                                                            (int64_t)bh * nsplit * kHeadDim) + lane;
+    auto partial_at = [&](int cc) {
+        if constexpr (kBf16) {
+            const uint32_t u = pob[(int64_t)cc * (kHeadDim / 2)];
+            return make_float2(bf16_lo(u), bf16_hi(u));
+        } else {
+            return po[(int64_t)cc * (kHeadDim / 2)];
+        }
+    };
+    float2 x[kMergeRegs];
 #pragma unroll
-    for (int i = 0; i < kMergeRegs; ++i) x[i] = p + P * i < nc ? po[(int64_t)(p + P * i) * kHeadDim] : 0.f;
+    for (int i = 0; i < kMergeRegs; ++i) x[i] = p + P * i < nc ? partial_at(p + P * i) : make_float2(0.f, 0.f);
     float mx = -INFINITY;
-    for (int cc = tid; cc < nc; cc += kHeadDim * P) mx = fmaxf(mx, pm[2 * cc]);
+    for (int cc = tid; cc < nc; cc += 64 * P) mx = fmaxf(mx, pm[2 * cc]);
     mx = wave_max(mx);
-    if ((tid & 63) == 0) red[tid >> 6] = mx;
+    if (lane == 0) red[p] = mx;
     __syncthreads();
     float M = red[0];
 #pragma unroll
-    for (int w = 1; w < kWaves; ++w) M = fmaxf(M, red[w]);
+    for (int w = 1; w < P; ++w) M = fmaxf(M, red[w]);
     float den = 0.f;
-    for (int cc = tid; cc < nc; cc += kHeadDim * P) {
+    for (int cc = tid; cc < nc; cc += 64 * P) {
         const float w = fast_exp2(pm[2 * cc] - M);
-        w_lds[cc] = w;
+        w_lds[cc] = kBf16 ? w * pm[2 * cc + 1] : w;  // a normalised partial weighs w l
         den += w * pm[2 * cc + 1];
     }
     den = wave_sum(den);
     __syncthreads();  // w_lds complete; red[] reads of the max are done
-    if ((tid & 63) == 0) red[tid >> 6] = den;
+    if (lane == 0) red[p] = den;
     __syncthreads();
     den = red[0];
 #pragma unroll
-    for (int w = 1; w < kWaves; ++w) den += red[w];
-    float num = 0.f;
+    for (int w = 1; w < P; ++w) den += red[w];
+    float n0 = 0.f, n1 = 0.f;
 #pragma unroll
-    for (int i = 0; i < kMergeRegs; ++i)
-        if (p + P * i < nc) num += w_lds[p + P * i] * x[i];
-    for (int cc = p + P * kMergeRegs; cc < nc; cc += P) num += w_lds[cc] * po[(int64_t)cc * kHeadDim];
-    if constexpr (P > 1) {
-        if (p > 0) part[p - 1][d] = num;
-        __syncthreads();
-        if (p > 0) return;
-#pragma unroll
-        for (int q = 0; q < P - 1; ++q) num += part[q][d];
+    for (int i = 0; i < kMergeRegs; ++i) {
+        if (p + P * i < nc) {
+            const float wc = w_lds[p + P * i];
+            n0 += wc * x[i].x;
+            n1 += wc * x[i].y;
+        }
     }
-    Elem<T>::store(out + (int64_t)bh * kHeadDim + d, num / den);
+    for (int cc = p + P * kMergeRegs; cc < nc; cc += P) {
+        const float2 v = partial_at(cc);
+        n0 += w_lds[cc] * v.x;
+        n1 += w_lds[cc] * v.y;
+    }
+    if (p > 0) part[p - 1][lane] = make_float2(n0, n1);
+    __syncthreads();
+    if (p > 0) return;
+#pragma unroll
+    for (int q = 0; q < P - 1; ++q) {
+        n0 += part[q][lane].x;
+        n1 += part[q][lane].y;
+    }
+    T* o = out + (int64_t)bh * kHeadDim + 2 * lane;
+    Elem<T>::store(o, n0 / den);
+    Elem<T>::store(o + 1, n1 / den);
 }
 
 // Kernel 2 for up to kMergeRegs splits: one wave per (sequence, q head), four
 // heads of a group per workgroup.  Lane l owns dims 2l and 2l+1 and lane c
 // holds split c's (m, l), so the max and the denominator are DPP wave
 // reductions and each split's weight reaches every lane by readlane: no LDS
-// and no barrier.  The sums run in the order of decode_merge_kernel<.., 1>.
+// and no barrier.
 // grid (groups, B, ceil(G / 4)), as the chunk kernel's (groups, B).
 template <typename T, int CH>
 __global__ __launch_bounds__(256) void decode_merge_wave_kernel(
@@ -435,20 +463,31 @@ __global__ __launch_bounds__(256) void decode_merge_wave_kernel(
     const int nc = (L + CH - 1) / CH;
     if (nc <= 1) return;  // written by the split kernel
     const float* pm = ws_ml + (int64_t)bh * nsplit * 2;
+    constexpr bool kBf16 = std::is_same<T, bf16_t>::value;
     const float2* po = reinterpret_cast<const float2*>(ws_o + (int64_t)bh * nsplit * kHeadDim) + lane;
+    const uint32_t* pob = reinterpret_cast<const uint32_t*>(reinterpret_cast<const bf16_t*>(ws_o) +
+                                                            (int64_t)bh * nsplit * kHeadDim) + lane;
     float2 x[kMergeRegs];
 #pragma unroll
-    for (int i = 0; i < kMergeRegs; ++i) x[i] = i < nc ? po[i * (kHeadDim / 2)] : make_float2(0.f, 0.f);
+    for (int i = 0; i < kMergeRegs; ++i) {
+        if constexpr (kBf16) {
+            const uint32_t u = i < nc ? pob[i * (kHeadDim / 2)] : 0u;
+            x[i] = make_float2(bf16_lo(u), bf16_hi(u));
+        } else {
+            x[i] = i < nc ? po[i * (kHeadDim / 2)] : make_float2(0.f, 0.f);
+        }
+    }
     const float m = lane < nc ? pm[2 * lane] : -INFINITY;
     const float l = lane < nc ? pm[2 * lane + 1] : 0.f;
     const float M = wave_max(m);
     const float w = lane < nc ? fast_exp2(m - M) : 0.f;
     const float den = wave_sum(w * l);
+    const float wn = kBf16 ? w * l : w;  // a normalised partial weighs w l
     float n0 = 0.f, n1 = 0.f;
 #pragma unroll
     for (int i = 0; i < kMergeRegs; ++i) {
         if (i < nc) {
-            const float wi = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, w), i));
+            const float wi = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wn), i));
             n0 += wi * x[i].x;
             n1 += wi * x[i].y;
         }
@@ -502,7 +541,7 @@ int launch_decode(const T* q, const T* kc, const T* vc, const ROWS& rows, const 
     const int n_rep = Hq / Hkv, G = pick_group(n_rep);
     const dim3 mgrid((unsigned)(Hkv * (n_rep / G)), (unsigned)B, (unsigned)G);
     if (nsplit > kMergeRegs)
-        hipLaunchKernelGGL((decode_merge_kernel<T, CH, 4>), mgrid, dim3(kHeadDim * 4), 0, st, ws_o, ws_ml, kv_len,
+        hipLaunchKernelGGL((decode_merge_kernel<T, CH, 8>), mgrid, dim3(64 * 8), 0, st, ws_o, ws_ml, kv_len,
                            max_kv, Hq, n_rep, nsplit, out);
     else if (nsplit > 1)
         hipLaunchKernelGGL((decode_merge_wave_kernel<T, CH>), dim3(mgrid.x, mgrid.y, (unsigned)((G + 3) / 4)), dim3(256),
