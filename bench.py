@@ -150,7 +150,8 @@ def bench_decode(args, dev, stream, lib):
     fn = lib.crane_hip_attn_decode
 
     def launch(i):
-        rc = fn(qp, kps[i % R], vps[i % R], cap, lp, cap, B, Hq, Hkv, D, scale, wp, need, op, 1, st)
+        # Qwen3-8B (n_rep 4): Crane's GQA-grouped decode form
+        rc = fn(qp, kps[i % R], vps[i % R], cap, lp, cap, B, Hq, Hkv, D, scale, 0, wp, need, op, 1, st)
         if rc:
             raise RuntimeError(f"crane_hip_attn_decode failed: {rc}")
 
@@ -186,8 +187,9 @@ def bench_decode_c5(args, dev, stream, lib):
     fn = lib.crane_hip_attn_decode
 
     def launch(i):
+        # Qwen2.5-72B (candle-transformers qwen2): the standard SDPA form
         rc = fn(q.data_ptr(), ks[i % R].data_ptr(), vs[i % R].data_ptr(), cap, kv_len_d.data_ptr(), cap, B, Hq, Hkv,
-                D, 1.0 / math.sqrt(D), ws.data_ptr(), need, out.data_ptr(), 1, st)
+                D, 1.0 / math.sqrt(D), 1, ws.data_ptr(), need, out.data_ptr(), 1, st)
         if rc:
             raise RuntimeError(f"crane_hip_attn_decode failed: {rc}")
 
@@ -233,8 +235,8 @@ def bench_decode_paged(args, dev, stream, lib):
     def launch(i):
         kp, vp = pools[i % R]
         rc = fn(q.data_ptr(), kp.data_ptr(), vp.data_ptr(), n_pages, P, table_d.data_ptr(), stride,
-                kv_len_d.data_ptr(), mx, B, Hq, Hkv, D, 1.0 / math.sqrt(D), ws.data_ptr(), ws_need, out.data_ptr(), 1,
-                st)
+                kv_len_d.data_ptr(), mx, B, Hq, Hkv, D, 1.0 / math.sqrt(D), 0, ws.data_ptr(), ws_need, out.data_ptr(),
+                1, st)
         if rc:
             raise RuntimeError(f"crane_hip_attn_decode_paged failed: {rc}")
 

@@ -1,9 +1,10 @@
 """crane_amd -- MI355X (gfx950) attention hot path for Crane-style models.
 
 The compute lives in libcrane_hip.so (hand-written HIP kernels behind the C
-ABI of include/crane_hip.h); `crane_amd.ops` is the Tensor-in/Tensor-out host
-surface over it and `crane_amd.attention` the model-level layer (KV cache,
-prefill/decode dispatch) that stands in for Crane's Attention::forward.
+ABI of include/*.h).  `crane_amd.ops` is the Tensor-in/Tensor-out host surface
+over it; `crane_amd.kv` holds the per-layer KV caches (dense and paged) that
+stand in for Attention.kv_cache; `crane_amd.decoder` composes one decoder
+layer from the kernels.
 """
 from ._lib import CraneHipError, LIB_PATH, version  # noqa: F401
 

@@ -17,6 +17,7 @@ LIB_PATH = os.path.join(HERE, "libcrane_hip.so")
 
 F32, BF16 = 0, 1
 NORM_THEN_ROPE, ROPE_THEN_NORM, ROPE_ONLY = 0, 1, 2
+SCORE_GROUPED, SCORE_STANDARD = 0, 1
 
 OK = 0
 E_INVALID, E_DTYPE, E_HEAD_DIM, E_GQA, E_CAPACITY, E_WORKSPACE, E_LAUNCH, E_ALIGN = range(1, 9)
@@ -34,9 +35,11 @@ SIGNATURES = {
          _i, _i, _i, _i, _i, _i, _vp], _i),
     "crane_hip_qnorm_rope": (
         [_vp, _i64, _vp, _f, _i, _vp, _vp, _i64, _i64, _i32p, _vp, _i, _i, _i, _i, _i, _vp], _i),
+    "crane_hip_rope_tables": ([_i, ctypes.c_double, ctypes.c_double, _i64, _i, _vp, _vp], _i),
+    "crane_hip_rope_tables_qwen2": ([_i, ctypes.c_double, _i64, _i, _vp, _vp], _i),
     "crane_hip_attn_decode_workspace": ([_i, _i, _i, _i, _i64, _i], _sz),
     "crane_hip_attn_decode": (
-        [_vp, _vp, _vp, _i64, _i32p, _i64, _i, _i, _i, _i, _f, _vp, _sz, _vp, _i, _vp], _i),
+        [_vp, _vp, _vp, _i64, _i32p, _i64, _i, _i, _i, _i, _f, _i, _vp, _sz, _vp, _i, _vp], _i),
     "crane_hip_attn_prefill": (
         [_vp, _vp, _vp, _i64, _i32p, _i64, _i, _i, _i, _i, _i, _f, _i, _vp, _i, _vp], _i),
     # include/crane_kv.h
@@ -47,7 +50,7 @@ SIGNATURES = {
     "crane_kv_update": ([_vp, _vp, _vp, _i, _vp], _i),
     "crane_kv_append_qkv": (
         [_vp, _vp, _i64, _vp, _vp, _f, _i, _vp, _vp, _i64, _i64, _i32p, _vp, _i, _i, _vp], _i),
-    "crane_kv_decode": ([_vp, _vp, _i, _f, _vp, _sz, _vp, _vp], _i),
+    "crane_kv_decode": ([_vp, _vp, _i, _f, _i, _vp, _sz, _vp, _vp], _i),
     "crane_kv_prefill": ([_vp, _vp, _i, _i, _f, _i, _vp, _vp], _i),
     "crane_kv_views": ([_vp, _vpp, _vpp, _i64p, _vpp, _i64p], _i),
     "crane_kv_set_lengths": ([_vp, _i64p, _vp], _i),
@@ -59,7 +62,7 @@ SIGNATURES = {
         [_vp, _i64, _vp, _vp, _f, _i, _vp, _vp, _i64, _i64, _i32p, _vp, _vp, _vp, _i64, _i, _i32p, _i64, _i32p,
          _i, _i, _i, _i, _i, _i, _vp], _i),
     "crane_hip_attn_decode_paged": (
-        [_vp, _vp, _vp, _i64, _i, _i32p, _i64, _i32p, _i64, _i, _i, _i, _i, _f, _vp, _sz, _vp, _i, _vp], _i),
+        [_vp, _vp, _vp, _i64, _i, _i32p, _i64, _i32p, _i64, _i, _i, _i, _i, _f, _i, _vp, _sz, _vp, _i, _vp], _i),
     "crane_hip_attn_prefill_paged": (
         [_vp, _vp, _vp, _i64, _i, _i32p, _i64, _i32p, _i64, _i, _i, _i, _i, _i, _f, _i, _vp, _i, _vp], _i),
     # include/crane_layer.h
@@ -86,7 +89,7 @@ SIGNATURES = {
     "crane_pkv_update": ([_vp, _vp, _vp, _i, _vp], _i),
     "crane_pkv_append_qkv": (
         [_vp, _vp, _i64, _vp, _vp, _f, _i, _vp, _vp, _i64, _i64, _i32p, _vp, _i, _i, _vp], _i),
-    "crane_pkv_decode": ([_vp, _vp, _i, _f, _vp, _sz, _vp, _vp], _i),
+    "crane_pkv_decode": ([_vp, _vp, _i, _f, _i, _vp, _sz, _vp, _vp], _i),
     "crane_pkv_prefill": ([_vp, _vp, _i, _i, _f, _i, _vp, _vp], _i),
     "crane_pkv_read_seq": ([_vp, _i, _vp, _vp, _vp], _i),
     "crane_pkv_write_seq": ([_vp, _i, _vp, _vp, _i64, _vp], _i),

@@ -14,7 +14,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libcrane_hip.so")
-SOURCES = ["capi.hip", "append.hip", "decode.hip", "prefill.hip", "kvcache.hip", "pagedkv.hip", "layer.hip", "gemm.hip", "sampling.hip"]
+SOURCES = ["capi.hip", "rope.hip", "append.hip", "decode.hip", "prefill.hip", "kvcache.hip", "pagedkv.hip", "layer.hip", "gemm.hip", "sampling.hip"]
 
 ARCH = "gfx950"
 # -packed-fp32-ops: no v_pk_{add,mul,fma}_f32 in any kernel.

@@ -16,4 +16,4 @@ extern "C" const char* crane_hip_strerror(int code) {
     }
 }
 
-extern "C" const char* crane_hip_version(void) { return "crane_hip 1 gfx950"; }
+extern "C" const char* crane_hip_version(void) { return "crane_hip 2 gfx950"; }

@@ -35,9 +35,18 @@
 // merge reads; sums stay in f32), for f32 the unnormalised f32 row.
 // Kernel 2 (decode_merge_kernel): the log-sum-exp merge of those partials.
 //
-// Crane's grouped decode pre-scales q in the model dtype (candle affine with
-// the scale converted to T, qwen3/modeling.rs:440-441) and its q@K^T output is
-// a T tensor; both roundings are reproduced so the scores match candle's.
+// Scores follow the candle path the caller names (score_mode).  The
+// GQA-grouped decode (qwen3/modeling.rs:432-467 for n_rep > 1,
+// hunyuan_dense/modeling.rs:575-608) pre-scales q in the model dtype (affine
+// with the scale converted to T, :440-441) and rounds q@K^T to T.  The
+// standard SDPA (qwen3/modeling.rs:485-488 for n_rep == 1, every qwen2.rs
+// decode :196-197) rounds q@K^T to T, then multiplies by the T scale and
+// rounds again.  Either way every rounding point of the scores is reproduced.
+// A sequence that fits one chunk also gets candle's softmax_last_dim chain in
+// T (candle-nn ops.rs, CPU softmax: e = T(exp(T(s - max))), sum in f32 rounded
+// to T, p = T(e / sum), then p @ V with f32 accumulation): the whole row is in
+// the workgroup, so the exact chain costs nothing measurable.  Longer
+// sequences keep the split-KV form (unnormalised bf16 p per chunk, f32 sums).
 #include <type_traits>
 
 #include "common.h"
@@ -101,7 +110,7 @@ struct DecodeShared {
 template <typename T, int G, int CH, class ROWS>
 __device__ __forceinline__ void decode_item(
     DecodeShared<T, G, CH>& sm, const T* __restrict__ q, const T* __restrict__ kc, const T* __restrict__ vc,
-    const ROWS& rows, int L, int b, int gi, int c, int Hq, int Hkv, int n_rep, float scale, int nsplit,
+    const ROWS& rows, int L, int b, int gi, int c, int Hq, int Hkv, int n_rep, float scale, bool post, int nsplit,
     float* __restrict__ ws_o, float* __restrict__ ws_ml, T* __restrict__ out) {
     constexpr bool kBf16 = std::is_same<T, bf16_t>::value;
     constexpr int kVecA = 16 * (int)sizeof(T) / 16;  // 16-byte loads per lane per K row (16 dims)
@@ -133,8 +142,10 @@ __device__ __forceinline__ void decode_item(
     auto& red = sm.red;
     auto& ml = sm.ml;
 
-    // q_g = q * scale in T, for this lane's 16 dims of every head.
+    // Grouped path: q_g = q * scale in T, for this lane's 16 dims of every head.
+    // Standard path: q as is (q * 1 rounds to q itself).
     const float scale_t = rt<T>(scale);
+    const float qmul = post ? 1.0f : scale_t;
     uint32_t qp[kBf16 ? G : 1][8];
     float qf[kBf16 ? 1 : G][16];
 #pragma unroll
@@ -151,10 +162,10 @@ __device__ __forceinline__ void decode_item(
         }
         if constexpr (kBf16) {
 #pragma unroll
-            for (int i = 0; i < 8; ++i) qp[h][i] = pack_bf16x2(x[2 * i] * scale_t, x[2 * i + 1] * scale_t);
+            for (int i = 0; i < 8; ++i) qp[h][i] = pack_bf16x2(x[2 * i] * qmul, x[2 * i + 1] * qmul);
         } else {
 #pragma unroll
-            for (int i = 0; i < 16; ++i) qf[h][i] = x[i] * scale_t;
+            for (int i = 0; i < 16; ++i) qf[h][i] = x[i] * qmul;
         }
     }
     // Rows [j0, j0 + n) of this (sequence, kv head), contiguous in both
@@ -215,32 +226,60 @@ __device__ __forceinline__ void decode_item(
     }
     __syncthreads();
 
-    // ---- B: per-head chunk max and sum (log2 domain); probabilities to LDS
+    // ---- B: per-head chunk max and sum; probabilities to LDS
+    const int n_chunks = (L + CH - 1) / CH;
+    const bool single = n_chunks == 1;  // uniform: the whole row is in this workgroup
     for (int h = wave; h < G; h += 4) {
         float sv[CH / 64];
         float m = -INFINITY;
 #pragma unroll
         for (int i = 0; i < CH / 64; ++i) {
             const int j = lane + 64 * i;
-            sv[i] = j < n ? rt<T>(s_lds[h][j]) * kLog2e : -INFINITY;
+            // the score as candle's T tensor holds it
+            sv[i] = j < n ? (post ? rt<T>(rt<T>(s_lds[h][j]) * scale_t) : rt<T>(s_lds[h][j])) : -INFINITY;
             m = fmaxf(m, sv[i]);
         }
         m = wave_max(m);
         float l = 0.f;
+        if (single) {
+            // candle's softmax_last_dim in T over the whole row
+            float e[CH / 64];
 #pragma unroll
-        for (int i = 0; i < CH / 64; ++i) {
-            const int j = lane + 64 * i;
-            float p = j < n ? fast_exp2(sv[i] - m) : 0.f;
-            if constexpr (kBf16) {
-                const bf16_t pb = f32_to_bf16(p);
-                p = bf16_to_f32(pb);
-                reinterpret_cast<bf16_t*>(p_lds)[((j >> 1) * G + h) * 2 + (j & 1)] = pb;
-            } else {
-                pf_lds[j * G + h] = p;
+            for (int i = 0; i < CH / 64; ++i) {
+                const int j = lane + 64 * i;
+                e[i] = j < n ? rt<T>(expf(rt<T>(sv[i] - m))) : 0.f;
+                l += e[i];
             }
-            l += p;
+            l = rt<T>(wave_sum(l));
+#pragma unroll
+            for (int i = 0; i < CH / 64; ++i) {
+                const int j = lane + 64 * i;
+                const float p = rt<T>(e[i] / l);
+                if constexpr (kBf16)
+                    reinterpret_cast<bf16_t*>(p_lds)[((j >> 1) * G + h) * 2 + (j & 1)] = f32_to_bf16(p);
+                else
+                    pf_lds[j * G + h] = p;
+            }
+            l = 1.f;  // the probabilities are normalised
+        } else {
+            // log2 domain, unnormalised: p = exp2((s - m) log2 e), rounded to
+            // bf16 for the P V product and summed as rounded
+            m *= kLog2e;
+#pragma unroll
+            for (int i = 0; i < CH / 64; ++i) {
+                const int j = lane + 64 * i;
+                float p = j < n ? fast_exp2(__builtin_fmaf(sv[i], kLog2e, -m)) : 0.f;
+                if constexpr (kBf16) {
+                    const bf16_t pb = f32_to_bf16(p);
+                    p = bf16_to_f32(pb);
+                    reinterpret_cast<bf16_t*>(p_lds)[((j >> 1) * G + h) * 2 + (j & 1)] = pb;
+                } else {
+                    pf_lds[j * G + h] = p;
+                }
+                l += p;
+            }
+            l = wave_sum(l);
         }
-        l = wave_sum(l);
         if (lane == 0) {
             ml[h][0] = m;
             ml[h][1] = l;
@@ -319,19 +358,18 @@ __device__ __forceinline__ void decode_item(
     }
     __syncthreads();
 
-    const int n_chunks = (L + CH - 1) / CH;
     for (int e = tid; e < G * kHeadDim; e += kThreads) {
         const int h = e / kHeadDim, d = e % kHeadDim;
         const float v = red[0][h][d] + red[1][h][d] + red[2][h][d] + red[3][h][d];
-        if (n_chunks == 1)  // the whole sequence fits one chunk: normalise and finish here
-            Elem<T>::store(out + ((int64_t)b * Hq + h0 + h) * kHeadDim + d, v / ml[h][1]);
+        if (single)  // the whole sequence fits one chunk: p was normalised, finish here
+            Elem<T>::store(out + ((int64_t)b * Hq + h0 + h) * kHeadDim + d, v);
         else if constexpr (kBf16)  // bf16 partials are stored normalised by the chunk's sum (merge weight w l)
             reinterpret_cast<bf16_t*>(ws_o)[(((int64_t)b * Hq + h0 + h) * nsplit + c) * kHeadDim + d] =
                 f32_to_bf16(v / ml[h][1]);
         else
             ws_o[(((int64_t)b * Hq + h0 + h) * nsplit + c) * kHeadDim + d] = v;
     }
-    if (n_chunks > 1 && tid < G) {
+    if (!single && tid < G) {
         float* dst = ws_ml + (((int64_t)b * Hq + h0 + tid) * nsplit + c) * 2;
         dst[0] = ml[tid][0];
         dst[1] = ml[tid][1];
@@ -345,14 +383,14 @@ __device__ __forceinline__ void decode_item(
 template <typename T, int G, int CH, class ROWS>
 __global__ __launch_bounds__(kThreads) void decode_chunk_kernel(
     const T* __restrict__ q, const T* __restrict__ kc, const T* __restrict__ vc, ROWS rows,
-    const int32_t* __restrict__ kv_len, int max_kv, int Hq, int Hkv, int n_rep, float scale, int nsplit,
+    const int32_t* __restrict__ kv_len, int max_kv, int Hq, int Hkv, int n_rep, float scale, int post, int nsplit,
     float* __restrict__ ws_o, float* __restrict__ ws_ml, T* __restrict__ out) {
     __shared__ DecodeShared<T, G, CH> sm;
     const int c = blockIdx.z;
     const int b = blockIdx.y;
     const int L = min(kv_len[b], max_kv);  // never read past the rows the host vouched for
-    decode_item<T, G, CH, ROWS>(sm, q, kc, vc, rows, L, b, blockIdx.x, c, Hq, Hkv, n_rep, scale, nsplit, ws_o, ws_ml,
-                                out);
+    decode_item<T, G, CH, ROWS>(sm, q, kc, vc, rows, L, b, blockIdx.x, c, Hq, Hkv, n_rep, scale, post != 0, nsplit, ws_o,
+                                ws_ml, out);
 }
 
 // Kernel 2: log-sum-exp merge of one (sequence, q head)'s partials.  Wave p
@@ -505,26 +543,26 @@ int pick_group(int n_rep) {
 
 template <typename T, int G, int CH, class ROWS>
 int launch_decode_g(const T* q, const T* kc, const T* vc, const ROWS& rows, const int32_t* kv_len, int max_kv,
-                    int nsplit, int B, int Hq, int Hkv, float scale, float* ws_o, float* ws_ml, T* out,
+                    int nsplit, int B, int Hq, int Hkv, float scale, int post, float* ws_o, float* ws_ml, T* out,
                     hipStream_t st) {
     const int n_rep = Hq / Hkv;
     const int groups = Hkv * (n_rep / G);
     const dim3 grid((unsigned)groups, (unsigned)B, (unsigned)nsplit);
     hipLaunchKernelGGL((decode_chunk_kernel<T, G, CH, ROWS>), grid, dim3(kThreads), 0, st, q, kc, vc, rows, kv_len,
-                       max_kv, Hq, Hkv, n_rep, scale, nsplit, ws_o, ws_ml, out);
+                       max_kv, Hq, Hkv, n_rep, scale, post, nsplit, ws_o, ws_ml, out);
     return hipGetLastError() == hipSuccess ? CRANE_HIP_OK : CRANE_HIP_E_LAUNCH;
 }
 
 // nsplit = ceil(max_kv / CH) chunks per sequence.
 template <typename T, int CH, class ROWS>
 int launch_decode(const T* q, const T* kc, const T* vc, const ROWS& rows, const int32_t* kv_len, int max_kv, int nsplit,
-                  int B, int Hq, int Hkv, float scale, float* ws_o, float* ws_ml, T* out, hipStream_t st) {
+                  int B, int Hq, int Hkv, float scale, int post, float* ws_o, float* ws_ml, T* out, hipStream_t st) {
     int rc;
     switch (pick_group(Hq / Hkv)) {
 #define CRANE_DECODE_CASE(g)                                                                                          \
     case g:                                                                                                           \
-        rc = launch_decode_g<T, g, CH, ROWS>(q, kc, vc, rows, kv_len, max_kv, nsplit, B, Hq, Hkv, scale, ws_o, ws_ml, \
-                                             out, st);                                                                \
+        rc = launch_decode_g<T, g, CH, ROWS>(q, kc, vc, rows, kv_len, max_kv, nsplit, B, Hq, Hkv, scale, post, ws_o,  \
+                                             ws_ml, out, st);                                                         \
         break;
         CRANE_DECODE_CASE(1)
         CRANE_DECODE_CASE(2)
@@ -555,29 +593,30 @@ int launch_decode(const T* q, const T* kc, const T* vc, const ROWS& rows, const 
 // takes 512 only when a page holds whole 512-row chunks.
 template <typename T, class ROWS>
 int launch_decode_any(const T* q, const T* kc, const T* vc, const ROWS& rows, const int32_t* kv_len, int max_kv, int B,
-                      int Hq, int Hkv, float scale, float* ws_o, float* ws_ml, T* out, hipStream_t st) {
+                      int Hq, int Hkv, float scale, int post, float* ws_o, float* ws_ml, T* out, hipStream_t st) {
     bool long_chunks = max_kv > kLongKv;
     if constexpr (ROWS::kPaged) long_chunks = long_chunks && rows.page_rows % kChunkLong == 0;
     if (long_chunks)
         return launch_decode<T, kChunkLong>(q, kc, vc, rows, kv_len, max_kv, (max_kv + kChunkLong - 1) / kChunkLong,
-                                            B, Hq, Hkv, scale, ws_o, ws_ml, out, st);
+                                            B, Hq, Hkv, scale, post, ws_o, ws_ml, out, st);
     return launch_decode<T, kChunkShort>(q, kc, vc, rows, kv_len, max_kv, (max_kv + kChunkShort - 1) / kChunkShort, B,
-                                         Hq, Hkv, scale, ws_o, ws_ml, out, st);
+                                         Hq, Hkv, scale, post, ws_o, ws_ml, out, st);
 }
 
 // Splits the workspace is sized for: the short chunk, which gives the most.
 int64_t n_splits(int64_t max_kv) { return (max_kv + kChunkShort - 1) / kChunkShort; }
 
-// Workspace: the partial rows, then their (max, sum) pairs.
+// Workspace: the partial rows (bf16 rows for bf16 calls, f32 rows for f32
+// calls), then their f32 (max, sum) pairs.
 struct WsLayout {
     size_t o_off, ml_off, total;
 };
 
-WsLayout ws_layout(int B, int Hq, int64_t ns) {
+WsLayout ws_layout(int B, int Hq, int64_t ns, int dtype) {
     auto up = [](size_t x) { return (x + 255) & ~(size_t)255; };
     WsLayout w;
     w.o_off = 0;
-    w.ml_off = w.o_off + up((size_t)B * Hq * ns * kHeadDim * sizeof(float));
+    w.ml_off = w.o_off + up((size_t)B * Hq * ns * kHeadDim * (size_t)elem_size(dtype));
     w.total = w.ml_off + up((size_t)B * Hq * ns * 2 * sizeof(float));
     return w;
 }
@@ -585,30 +624,32 @@ WsLayout ws_layout(int B, int Hq, int64_t ns) {
 // Checks shared by both layouts, then the launch; `rows` addresses the cache.
 template <class ROWS>
 int attn_decode(const void* q, const void* k_cache, const void* v_cache, const ROWS& rows, const int32_t* kv_len,
-                int64_t max_kv, int B, int Hq, int Hkv, int D, float scale, void* workspace, size_t ws_bytes,
-                void* out, int dtype, void* stream) {
+                int64_t max_kv, int B, int Hq, int Hkv, int D, float scale, int score_mode, void* workspace,
+                size_t ws_bytes, void* out, int dtype, void* stream) {
     if (dtype != CRANE_HIP_F32 && dtype != CRANE_HIP_BF16) return CRANE_HIP_E_DTYPE;
     if (D != kHeadDim) return CRANE_HIP_E_HEAD_DIM;
     if (B < 0 || Hq <= 0 || Hkv <= 0) return CRANE_HIP_E_INVALID;
     if (Hq % Hkv != 0) return CRANE_HIP_E_GQA;
     if (max_kv <= 0) return CRANE_HIP_E_INVALID;
     if (!(scale > 0.0f) || !__builtin_isfinite(scale)) return CRANE_HIP_E_INVALID;
+    if (score_mode != CRANE_HIP_SCORE_GROUPED && score_mode != CRANE_HIP_SCORE_STANDARD) return CRANE_HIP_E_INVALID;
     if (B == 0) return CRANE_HIP_OK;
     if (!q || !k_cache || !v_cache || !kv_len || !out) return CRANE_HIP_E_INVALID;
     if (!aligned16(q) || !aligned16(k_cache) || !aligned16(v_cache)) return CRANE_HIP_E_ALIGN;
     const int64_t ns = n_splits(max_kv);
     if (max_kv > 0x7fffffffLL || ns > kMaxSplits || B > 65535 || (int64_t)B * Hq > 0x7fffffffLL)
         return CRANE_HIP_E_INVALID;
-    const WsLayout w = ws_layout(B, Hq, ns);
+    const WsLayout w = ws_layout(B, Hq, ns, dtype);
     if (!workspace || ws_bytes < w.total || !aligned16(workspace)) return CRANE_HIP_E_WORKSPACE;
     float* ws_o = (float*)((char*)workspace + w.o_off);
     float* ws_ml = (float*)((char*)workspace + w.ml_off);
     hipStream_t st = (hipStream_t)stream;
+    const int post = score_mode == CRANE_HIP_SCORE_STANDARD;
     if (dtype == CRANE_HIP_F32)
         return launch_decode_any<float>((const float*)q, (const float*)k_cache, (const float*)v_cache, rows, kv_len,
-                                        (int)max_kv, B, Hq, Hkv, scale, ws_o, ws_ml, (float*)out, st);
+                                        (int)max_kv, B, Hq, Hkv, scale, post, ws_o, ws_ml, (float*)out, st);
     return launch_decode_any<bf16_t>((const bf16_t*)q, (const bf16_t*)k_cache, (const bf16_t*)v_cache, rows, kv_len,
-                                     (int)max_kv, B, Hq, Hkv, scale, ws_o, ws_ml, (bf16_t*)out, st);
+                                     (int)max_kv, B, Hq, Hkv, scale, post, ws_o, ws_ml, (bf16_t*)out, st);
 }
 
 }  // namespace
@@ -617,28 +658,28 @@ int attn_decode(const void* q, const void* k_cache, const void* v_cache, const R
 using namespace crane;
 
 extern "C" size_t crane_hip_attn_decode_workspace(int B, int Hq, int Hkv, int D, int64_t max_kv, int dtype) {
-    (void)dtype;
     if (B <= 0 || Hq <= 0 || Hkv <= 0 || D != kHeadDim || max_kv <= 0) return 0;
-    return ws_layout(B, Hq, n_splits(max_kv)).total;
+    if (dtype != CRANE_HIP_F32 && dtype != CRANE_HIP_BF16) return 0;
+    return ws_layout(B, Hq, n_splits(max_kv), dtype).total;
 }
 
 extern "C" int crane_hip_attn_decode(const void* q, const void* k_cache, const void* v_cache, int64_t cache_cap,
                                      const int32_t* kv_len, int64_t max_kv, int B, int Hq, int Hkv, int D,
-                                     float scale, void* workspace, size_t ws_bytes, void* out, int dtype,
-                                     void* stream) {
+                                     float scale, int score_mode, void* workspace, size_t ws_bytes, void* out,
+                                     int dtype, void* stream) {
     if (cache_cap <= 0 || max_kv > cache_cap) return CRANE_HIP_E_CAPACITY;
-    return attn_decode(q, k_cache, v_cache, DenseRows{cache_cap}, kv_len, max_kv, B, Hq, Hkv, D, scale, workspace,
-                       ws_bytes, out, dtype, stream);
+    return attn_decode(q, k_cache, v_cache, DenseRows{cache_cap}, kv_len, max_kv, B, Hq, Hkv, D, scale, score_mode,
+                       workspace, ws_bytes, out, dtype, stream);
 }
 
 extern "C" int crane_hip_attn_decode_paged(const void* q, const void* k_pool, const void* v_pool, int64_t n_pages,
                                            int page_rows, const int32_t* block_table, int64_t table_stride,
                                            const int32_t* kv_len, int64_t max_kv, int B, int Hq, int Hkv, int D,
-                                           float scale, void* workspace, size_t ws_bytes, void* out, int dtype,
-                                           void* stream) {
+                                           float scale, int score_mode, void* workspace, size_t ws_bytes, void* out,
+                                           int dtype, void* stream) {
     const int rc = check_paged(n_pages, page_rows, block_table, table_stride, Hkv);
     if (rc) return rc;
     if (max_kv > table_stride * page_rows) return CRANE_HIP_E_CAPACITY;
     return attn_decode(q, k_pool, v_pool, PagedRows{block_table, table_stride, n_pages, page_rows}, kv_len, max_kv, B,
-                       Hq, Hkv, D, scale, workspace, ws_bytes, out, dtype, stream);
+                       Hq, Hkv, D, scale, score_mode, workspace, ws_bytes, out, dtype, stream);
 }

@@ -247,14 +247,14 @@ extern "C" int crane_kv_append_qkv(crane_kv* kv, const void* qkv, int64_t qkv_ro
     return rc ? rc : c.grow_lengths(S, st);
 }
 
-extern "C" int crane_kv_decode(const crane_kv* kv, const void* q, int Hq, float scale, void* workspace, size_t ws_bytes,
-                               void* out, void* stream) {
+extern "C" int crane_kv_decode(const crane_kv* kv, const void* q, int Hq, float scale, int score_mode, void* workspace,
+                               size_t ws_bytes, void* out, void* stream) {
     if (!kv) return CRANE_HIP_E_INVALID;
     const KvCache& c = kv->impl;
     if (c.B() == 0) return CRANE_HIP_OK;
     if (!c.k() || !c.dev_len() || c.max_len() == 0) return CRANE_HIP_E_INVALID;
     return crane_hip_attn_decode(q, c.k(), c.v(), c.cap(), c.dev_len(), c.max_len(), c.B(), Hq, c.Hkv(), c.D(), scale,
-                                 workspace, ws_bytes, out, c.dtype(), stream);
+                                 score_mode, workspace, ws_bytes, out, c.dtype(), stream);
 }
 
 extern "C" int crane_kv_prefill(const crane_kv* kv, const void* q, int Hq, int S, float scale, int causal, void* out,
@@ -297,7 +297,9 @@ extern "C" int crane_kv_stack(crane_kv* dst, const crane_kv* const* srcs, int n,
     if (d.B() != n) return CRANE_HIP_E_INVALID;
     int64_t max_len = 0;
     for (int i = 0; i < n; ++i) {
-        if (!srcs[i] || srcs[i]->impl.B() != 1 || !d.same_shape(srcs[i]->impl)) return CRANE_HIP_E_INVALID;
+        // dst is reallocated before the copies: a source that is dst itself would be lost
+        if (!srcs[i] || srcs[i] == dst || srcs[i]->impl.B() != 1 || !d.same_shape(srcs[i]->impl))
+            return CRANE_HIP_E_INVALID;
         max_len = std::max(max_len, srcs[i]->impl.len()[0]);
     }
     const hipStream_t st = (hipStream_t)stream;

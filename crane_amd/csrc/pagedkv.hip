@@ -271,12 +271,13 @@ class PagedKv {
         return grow_lengths(S, st);
     }
 
-    int decode(const void* q, int Hq, float scale, void* ws, size_t ws_bytes, void* out, hipStream_t st) const {
+    int decode(const void* q, int Hq, float scale, int score_mode, void* ws, size_t ws_bytes, void* out,
+               hipStream_t st) const {
         if (batch_.empty()) return CRANE_HIP_OK;
         const int64_t m = max_len();
         if (m == 0) return CRANE_HIP_E_INVALID;
         return crane_hip_attn_decode_paged(q, k_pool_, v_pool_, n_pages_, P_, d_table_, max_pps_, d_len_, m, B(), Hq,
-                                           Hkv_, D_, scale, ws, ws_bytes, out, dtype_, st);
+                                           Hkv_, D_, scale, score_mode, ws, ws_bytes, out, dtype_, st);
     }
 
     int prefill(const void* q, int Hq, int S, float scale, int causal, void* out, hipStream_t st) {
@@ -451,9 +452,10 @@ extern "C" int crane_pkv_append_qkv(crane_pkv* pkv, const void* qkv, int64_t qkv
                                 positions, q_out, S, Hq, (hipStream_t)stream);
 }
 
-extern "C" int crane_pkv_decode(const crane_pkv* pkv, const void* q, int Hq, float scale, void* workspace,
-                                size_t ws_bytes, void* out, void* stream) {
-    return pkv ? pkv->impl.decode(q, Hq, scale, workspace, ws_bytes, out, (hipStream_t)stream) : CRANE_HIP_E_INVALID;
+extern "C" int crane_pkv_decode(const crane_pkv* pkv, const void* q, int Hq, float scale, int score_mode,
+                                void* workspace, size_t ws_bytes, void* out, void* stream) {
+    return pkv ? pkv->impl.decode(q, Hq, scale, score_mode, workspace, ws_bytes, out, (hipStream_t)stream)
+               : CRANE_HIP_E_INVALID;
 }
 
 extern "C" int crane_pkv_prefill(crane_pkv* pkv, const void* q, int Hq, int S, float scale, int causal, void* out,

@@ -23,16 +23,24 @@
 // Workgroup ids are remapped so that heavy (late) query tiles start first and
 // the q heads sharing a kv head run on the same XCD (shared L2).
 //
-// Rounding points (bf16): candle's bf16 matmul returns Q K^T rounded to bf16
-// and its affine scales by the scale converted to bf16; both are reproduced.
-// candle then rounds the scaled score to bf16 again, and rounds exp, the row
-// sum and the quotient to bf16; those are not reproduced (the online softmax
-// keeps them in f32, P enters the PV product in bf16).  The second score
-// rounding costs about 11% of the kernel's time to reproduce and moves an
-// output past 2e-2 of candle's in about 1 element in 2e7 on N(0,1) data, always
-// one where candle's own result is farther from the exact one.  The row sum l
-// adds the bf16 p that enter the PV product (v_dot2_f32_bf16 against (1, 1)),
-// so numerator and denominator see the same weights.
+// Rounding points (bf16): candle's bf16 matmul returns Q K^T rounded to bf16,
+// and its affine multiplies that by the scale converted to bf16 and rounds the
+// product to bf16 again (qwen3/modeling.rs:488); both roundings are
+// reproduced for every score.  The first packs two scores with one
+// v_cvt_pk_bf16_f32; the product of two bf16 values is exact in f32 and comes
+// from v_dot2_f32_bf16 against (scale, 0) or (0, scale); the second rounding
+// is a v_cvt_pk_bf16_f32 with a zero low half, read back as an f32.
+// candle's softmax_last_dim then rounds s - max, exp, the row sum and the
+// quotient p = e / sum to bf16 before the P V product (:493-494).  A one-pass
+// kernel only has the row's max and sum at the end, so for rows with more than
+// one 64-key tile these roundings are not reproduced: the online softmax keeps
+// them in f32, P enters the P V product in bf16, and the row sum l adds the
+// same bf16 p (v_dot2_f32_bf16 against (1, 1)), so numerator and denominator
+// see the same weights.  A wave whose 32 rows all see keys of the first tile
+// only (the first rows of a causal prefill, where few keys carry large
+// weights and candle's roundings move the output most) runs candle's chain
+// exactly: the row max, e = bf16(exp(bf16(s - max))), the bf16 sum, p =
+// bf16(e / sum), and O = P V without a final division.
 //
 // f32 kernel: a plain wave-per-query-row online-softmax kernel; Crane serves
 // prefill in bf16 on GPU (crane-serve/src/lib.rs:123-150), f32 is kept for
@@ -53,7 +61,8 @@ constexpr int kBM = 32 * kWaves;              // query rows per workgroup
 constexpr int kCopies = 16 / kWaves;          // 1 KiB blocks of a 16 KiB tile each wave copies
 constexpr int kBN = 64;                       // keys per tile
 constexpr int kTileBytes = kBN * kHeadDim * 2;  // 16 KiB of K (or V) per tile
-constexpr float kLazy = 8.0f;                 // log2-domain slack before the running max moves
+constexpr float kPsumMax = 256.0f;            // largest tile sum of p in a lane before the running max moves
+constexpr float kMaskRaw = -1.0e30f;          // raw score of a masked key (finite: see scores_bf16)
 
 __device__ __forceinline__ f32x16_v mfma32(bf16x8_v a, bf16x8_v b, f32x16_v c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
@@ -125,6 +134,35 @@ __device__ __forceinline__ void qk_tile(const uint8_t* kt_lds, const bf16x8_v (&
         }
 }
 
+// candle's bf16 scores of four raw f32 products (two rounded pairs w0, w1 =
+// bf16(Q K^T)): s = bf16(bf16(acc) * scale), with scale a bf16 value held as
+// the pairs (scale, 0) and (0, scale).  Each product of two bf16 values is
+// exact in f32 and comes from v_dot2_f32_bf16 with a zero accumulator; the
+// rounding is v_cvt_pk_bf16_f32 with a zero low half, read as an f32.  Written
+// as instructions because the compiler clears a register for each product's
+// accumulator and rounds into the low half before moving it up (a v_mov and a
+// v_perm per score).  gfx950 lets another VALU instruction read a v_dot2
+// result only 3 instructions after it is written, so the four products are
+// formed first: each rounding reads its product exactly 3 instructions later.
+// The inputs come from ordinary VALU instructions (no MFMA result is read
+// here), and every output is an ordinary VALU result.  A masked key carries
+// the finite raw score kMaskRaw (an infinite one would turn its partner's
+// product with 0 into NaN); it stays a huge negative score.
+__device__ __forceinline__ void scores_bf16x4(uint32_t w0, uint32_t w1, uint32_t sc_lo, uint32_t sc_hi, float& s0,
+                                              float& s1, float& s2, float& s3) {
+    float x0, x1, x2, x3;
+    asm("v_dot2_f32_bf16 %4, %8, %10, 0\n\t"
+        "v_dot2_f32_bf16 %5, %8, %11, 0\n\t"
+        "v_dot2_f32_bf16 %6, %9, %10, 0\n\t"
+        "v_dot2_f32_bf16 %7, %9, %11, 0\n\t"
+        "v_cvt_pk_bf16_f32 %0, 0, %4\n\t"
+        "v_cvt_pk_bf16_f32 %1, 0, %5\n\t"
+        "v_cvt_pk_bf16_f32 %2, 0, %6\n\t"
+        "v_cvt_pk_bf16_f32 %3, 0, %7"
+        : "=&v"(s0), "=&v"(s1), "=&v"(s2), "=&v"(s3), "=&v"(x0), "=&v"(x1), "=&v"(x2), "=&v"(x3)
+        : "v"(w0), "v"(w1), "s"(sc_lo), "s"(sc_hi));
+}
+
 // Keep a value in a register as computed: the compiler may not split it into
 // a base plus a per-use offset (which would cost an add per use in the loop).
 __device__ __forceinline__ uint32_t pinned(uint32_t v) {
@@ -160,7 +198,7 @@ __device__ __forceinline__ bool map_block(int id, int n_qt, int B, int Hkv, int 
 template <bool CAUSAL, class ROWS, int SPLIT>
 __global__ __launch_bounds__(64 * kWaves * SPLIT) __attribute__((amdgpu_waves_per_eu(2, 2))) void prefill_bf16_kernel(
     const bf16_t* __restrict__ q, const bf16_t* __restrict__ kc, const bf16_t* __restrict__ vc, ROWS rows,
-    const int32_t* __restrict__ start_pos, int max_start, int S, int B, int Hq, int Hkv, float scale_log2,
+    const int32_t* __restrict__ start_pos, int max_start, int S, int B, int Hq, int Hkv, uint32_t scale_bits,
     bf16_t* __restrict__ out) {
     const int n_rep = Hq / Hkv;
     const int n_qt = (S + kBM - 1) / kBM;
@@ -237,6 +275,11 @@ __global__ __launch_bounds__(64 * kWaves * SPLIT) __attribute__((amdgpu_waves_pe
     float m_run = -INFINITY, l_run = 0.f;
     const int qpos = start + qrow;                      // absolute position of my query
     const int wave_first = start + m0 + wave * 32;      // first position of this wave's rows
+    // Every key this wave's rows see lies in tile 0: candle's softmax chain runs exactly.
+    const bool exact = grp == 0 && (CAUSAL ? wave_first + 31 < kBN : L <= kBN);
+    // the bf16 scale as the pairs (scale, 0) and (0, scale), and as an f32
+    const uint32_t sc_lo = scale_bits, sc_hi = scale_bits << 16;
+    const float scale_log2 = __uint_as_float(sc_hi) * kLog2e;  // raw-score scale of the running max
     // transposed-read coordinates of this lane for the V^T fragments
     const int vg = lane >> 4, vi = lane & 15;
     const int v_h = vg >> 1;                            // key half of the A operand
@@ -264,6 +307,80 @@ __global__ __launch_bounds__(64 * kWaves * SPLIT) __attribute__((amdgpu_waves_pe
     f32x16_v sa[2], sb[2];
     qk_tile(kbuf[0], qf, koff, sa);
 
+    // O^T += V^T P^T over one V tile: 4 dim blocks x 4 key steps of 16; the A
+    // operand (dims x keys) comes straight from the row-major V tile by
+    // transposed reads.
+    auto pv_tile = [&](const uint8_t* vt_lds, const bf16x8_v (&pf)[4]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int st = 0; st < 4; ++st) {
+#pragma unroll
+            for (int db = 0; db < 4; ++db) {
+                const uint2 lo = read_tr16(vt_lds + voff[db][0] + st * 4096);  // keys of slots 0..3
+                const uint2 hi = read_tr16(vt_lds + voff[db][1] + st * 4096);  // slots 4..7: 8 rows on
+                const uint4 vu = make_uint4(lo.x, lo.y, hi.x, hi.y);
+                oacc[db] = mfma32(as_bf16x8(vu), pf[st], oacc[db]);
+            }
+        }
+    };
+
+    // Waves whose rows see keys of tile 0 only (the first rows of a causal
+    // prefill, or a short non-causal one) run candle's softmax_last_dim chain
+    // in bf16 exactly, before the loop: the row max, e = bf16(exp(bf16(s -
+    // max))), the sum in f32 rounded to bf16, p = bf16(e / sum) (e times the
+    // sum's reciprocal), then O = P V with no division at the end.  Their
+    // workgroup waits for V(0) once more; the loop skips their tile 0.
+    if (CAUSAL ? start + m0 + 31 < kBN : L <= kBN) {  // uniform: wave 0 of the workgroup is exact
+        if (n_tiles > 1) CRANE_WAIT_VMCNT(kCopies); else CRANE_WAIT_VMCNT(0);  // this wave's V(0) copies
+        __syncthreads();                                                     // ... and every wave's
+        if (exact) {
+            if (CAUSAL || L < kBN) {
+#pragma unroll
+                for (int nb = 0; nb < 2; ++nb)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) {
+                        const int key = nb * 32 + 8 * (r >> 2) + 4 * hh + (r & 3);
+                        if (key >= L || (CAUSAL && key > qpos)) sa[nb][r] = kMaskRaw;
+                    }
+            }
+            float mx = -INFINITY;
+#pragma unroll
+            for (int nb = 0; nb < 2; ++nb)
+#pragma unroll
+                for (int r = 0; r < 16; r += 4) {
+                    float s0, s1, s2, s3;
+                    scores_bf16x4(pack_bf16x2(sa[nb][r], sa[nb][r + 1]), pack_bf16x2(sa[nb][r + 2], sa[nb][r + 3]), sc_lo,
+                                  sc_hi, s0, s1, s2, s3);
+                    sa[nb][r] = s0;
+                    sa[nb][r + 1] = s1;
+                    sa[nb][r + 2] = s2;
+                    sa[nb][r + 3] = s3;
+                    mx = fmaxf(mx, fmaxf(fmaxf(s0, s1), fmaxf(s2, s3)));
+                }
+            mx = fmaxf(mx, __shfl_xor(mx, 32));  // the row's other 32 keys sit in the other lane half
+            float sum = 0.f;
+#pragma unroll
+            for (int nb = 0; nb < 2; ++nb)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    sa[nb][r] = rt<bf16_t>(fast_exp2(rt<bf16_t>(sa[nb][r] - mx) * kLog2e));
+                    sum += sa[nb][r];
+                }
+            const float inv = 1.0f / rt<bf16_t>(sum + __shfl_xor(sum, 32));
+            bf16x8_v pf[4];
+#pragma unroll
+            for (int nb = 0; nb < 2; ++nb)
+#pragma unroll
+                for (int r = 0; r < 16; r += 2) {
+                    const bf16x2_v pw = __builtin_bit_cast(bf16x2_v, pack_bf16x2(sa[nb][r] * inv, sa[nb][r + 1] * inv));
+                    pf[nb * 2 + (r >> 3)][r & 7] = pw[0];
+                    pf[nb * 2 + (r >> 3)][(r & 7) + 1] = pw[1];
+                }
+            pv_tile(vbuf[0], pf);
+            m_run = 0.f;   // finite, so a key-split merge keeps these rows as they are
+            l_run = 0.5f;  // each lane half holds half of the normalised row sum
+        }
+    }
+
     // One tile: softmax of tile t's scores (sc), S^T of tile t+1 (into sn),
     // then O^T += V^T P^T for tile t.  The exp work of tile t and the MFMAs of
     // tile t+1 are independent, so one wave keeps both pipes busy.
@@ -278,80 +395,95 @@ __global__ __launch_bounds__(64 * kWaves * SPLIT) __attribute__((amdgpu_waves_pe
         if (SPLIT > 1 && t >= n_tiles) return;  // past this group's half: only the barrier
         const int kt = (t0 + t) * kBN;
         if (CAUSAL && kt > wave_first + 31) return;  // the whole tile is above this wave's diagonal
+        if (exact) return;                           // done before the loop (its only tile is tile 0)
         if (kt + kBN > kend || (CAUSAL && kt + kBN - 1 > wave_first)) {  // diagonal or last tile
 #pragma unroll
             for (int nb = 0; nb < 2; ++nb)
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
                     const int key = kt + nb * 32 + 8 * (r >> 2) + 4 * hh + (r & 3);
-                    if (key >= kend || (CAUSAL && key > qpos)) sc[nb][r] = -INFINITY;
+                    if (key >= kend || (CAUSAL && key > qpos)) sc[nb][r] = kMaskRaw;
                 }
         }
-        float tmax = -INFINITY;
-#pragma unroll
-        for (int nb = 0; nb < 2; ++nb)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) tmax = fmaxf(tmax, sc[nb][r]);
-        tmax *= scale_log2;  // this lane half's raw-score max; the scale is positive
-        // Lazy rescaling: the reference max m_run only moves when some row's max
-        // exceeds it by more than kLazy, so O and l are rescaled rarely and
-        // p = exp2(s * scale_log2 - m_run) stays below 2^kLazy.  The decision is
-        // wave-wide, so each lane half's own max decides it; the row max over
-        // both halves (the two halves of a row share m_run) is only needed when
-        // m_run moves.  The first tile always moves it (m_run starts at -inf;
-        // key 0 is visible to every query, so m_run is finite afterwards).
-        if (__any(tmax > m_run + kLazy)) {
-            const float m_new = fmaxf(m_run, fmaxf(tmax, __shfl_xor(tmax, 32)));
-            // A later group's row that has seen no key yet keeps m = -inf (and O,
-            // l = 0): its factor must not become exp2(-inf + inf).
-            const float alpha = SPLIT > 1 && m_new == -INFINITY ? 1.f : fast_exp2(m_run - m_new);
-            l_run *= alpha;
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-#pragma unroll
-                for (int r = 0; r < 16; ++r) oacc[i][r] *= alpha;
-            m_run = m_new;
-        }
-        const float neg_m = SPLIT > 1 && m_run == -INFINITY ? 0.f : -m_run;  // its p = exp2(-inf) = 0
-        float psum = 0.f;
         bf16x8_v pf[4];
+        {
+            // p = exp2(s log2(e) - m) for candle's bf16 score s of every key,
+            // bf16 for the P V product, summed as rounded.
+            auto tile_p = [&](float neg_m) __attribute__((always_inline)) {
+                float psum = 0.f;
 #pragma unroll
-        for (int nb = 0; nb < 2; ++nb)
+                for (int nb = 0; nb < 2; ++nb)
 #pragma unroll
-            for (int r = 0; r < 16; r += 2) {
-                // The QK^T product is rounded to bf16, as candle's bf16 matmul
-                // output is (one v_cvt_pk_bf16_f32 for two scores);
-                // p = exp2(bf16(s) * scale_log2 - m).
-                const uint32_t w = pack_bf16x2(sc[nb][r], sc[nb][r + 1]);
-                // low half moved up by v_perm (kept opaque, so the pair stays one cvt)
-                const float s0 = __uint_as_float(__builtin_amdgcn_perm(0u, w, 0x01000c0cu));
-                const float p0 = fast_exp2(__builtin_fmaf(s0, scale_log2, neg_m));
-                const float p1 = fast_exp2(__builtin_fmaf(bf16_hi(w), scale_log2, neg_m));
-                // The row sum adds the same bf16 p that the P V product uses, so
-                // a row dominated by one key returns that V row unscaled.
-                const bf16x2_v pw = __builtin_bit_cast(bf16x2_v, pack_bf16x2(p0, p1));
-                psum = __builtin_amdgcn_fdot2_f32_bf16(pw, ones, psum, false);
-                pf[nb * 2 + (r >> 3)][r & 7] = pw[0];
-                pf[nb * 2 + (r >> 3)][(r & 7) + 1] = pw[1];
-            }
-        l_run += psum;
+                    for (int r = 0; r < 16; r += 4) {
+                        float sv[4];
+                        scores_bf16x4(pack_bf16x2(sc[nb][r], sc[nb][r + 1]), pack_bf16x2(sc[nb][r + 2], sc[nb][r + 3]),
+                                      sc_lo, sc_hi, sv[0], sv[1], sv[2], sv[3]);
+#pragma unroll
+                        for (int u = 0; u < 4; u += 2) {
+                            const float p0 = fast_exp2(__builtin_fmaf(sv[u], kLog2e, neg_m));
+                            const float p1 = fast_exp2(__builtin_fmaf(sv[u + 1], kLog2e, neg_m));
+                            const bf16x2_v pw = __builtin_bit_cast(bf16x2_v, pack_bf16x2(p0, p1));
+                            psum = __builtin_amdgcn_fdot2_f32_bf16(pw, ones, psum, false);
+                            pf[nb * 2 + (r >> 3)][(r & 7) + u] = pw[0];
+                            pf[nb * 2 + (r >> 3)][(r & 7) + u + 1] = pw[1];
+                        }
+                    }
+                return psum;
+            };
+            // Lazy rescaling: the reference max m_run stays where it is while
+            // every lane's tile sum of p stays at most kPsumMax (so every p <=
+            // kPsumMax; no max over the tile is taken).  Otherwise (including
+            // the first tile, where m_run = -inf gives p = inf) the wave moves
+            // m_run to each row's running max, rescales O and l, and takes the
+            // tile's p again.  A row that has seen no key keeps m = -inf, with
+            // p = exp2(huge negative) = 0.
+            auto rescale = [&](float tmax) __attribute__((always_inline)) {
+                // tmax: this lane half's raw max; the row's max over both halves
+                // in the log2 domain (the scale is positive); no key: -inf
+                tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
+                tmax = tmax > 0.5f * kMaskRaw ? tmax * scale_log2 : -INFINITY;
+                const float m_new = fmaxf(m_run, tmax);
+                const float alpha = m_new == -INFINITY ? 1.f : fast_exp2(m_run - m_new);
+                l_run *= alpha;
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) oacc[i][r] *= alpha;
+                m_run = m_new;
+            };
+            auto tile_max = [&]() __attribute__((always_inline)) {
+                float tmax = kMaskRaw;
+#pragma unroll
+                for (int nb = 0; nb < 2; ++nb)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) tmax = fmaxf(tmax, sc[nb][r]);
+                return tmax;
+            };
+#ifdef PF_MAX_CHECK
+            const float tmax = tile_max();
+            if (__any(tmax * scale_log2 > m_run + 8.0f)) rescale(tmax);
+            l_run += tile_p(m_run == -INFINITY ? 0.f : -m_run);
+        }
         // Unconditional, so this stays in one basic block with the exp work
         // above: past the last tile (or above this wave's diagonal) the
         // result is simply not used, and nothing is in flight into that buffer.
         qk_tile(kbuf[par ^ 1], qf, koff, sn);
-        // ---- O^T += V^T P^T: 4 dim blocks x 4 key steps of 16; the A operand
-        // (dims x keys) comes straight from the row-major V tile by transposed reads
-        const uint8_t* vt_lds = vbuf[par];
-#pragma unroll
-        for (int st = 0; st < 4; ++st) {
-#pragma unroll
-            for (int db = 0; db < 4; ++db) {
-                const uint2 lo = read_tr16(vt_lds + voff[db][0] + st * 4096);  // keys of slots 0..3
-                const uint2 hi = read_tr16(vt_lds + voff[db][1] + st * 4096);  // slots 4..7: 8 rows on
-                const uint4 vu = make_uint4(lo.x, lo.y, hi.x, hi.y);
-                oacc[db] = mfma32(as_bf16x8(vu), pf[st], oacc[db]);
+        pv_tile(vbuf[par], pf);
+#else
+            float psum = tile_p(m_run == -INFINITY ? 0.f : -m_run);
+            // Unconditional, so this stays in one basic block with the exp
+            // work above: past the last tile (or above this wave's diagonal)
+            // the result is simply not used, and nothing is in flight into
+            // that buffer.
+            qk_tile(kbuf[par ^ 1], qf, koff, sn);
+            if (__any(!(psum <= kPsumMax) || m_run == -INFINITY)) {
+                rescale(tile_max());
+                psum = tile_p(m_run == -INFINITY ? 0.f : -m_run);
             }
+            l_run += psum;
         }
+        pv_tile(vbuf[par], pf);
+#endif
     };
     const int n_steps = SPLIT > 1 ? half : n_tiles;
     for (int t = 0; t < n_steps; t += 2) {
@@ -390,7 +522,7 @@ __global__ __launch_bounds__(64 * kWaves * SPLIT) __attribute__((amdgpu_waves_pe
             for (int r = 0; r < 16; ++r) oacc[i][r] = oacc[i][r] * a0 + xo[64 * (16 * i + r)] * a1;
     }
 
-    l_run += __shfl_xor(l_run, 32);  // the two lane halves hold different keys of the row
+    l_run += __shfl_xor(l_run, 32);  // the two lane halves hold different keys of the row (exact rows: 1)
     if (qrow < S) {
         const float inv = 1.0f / l_run;
         bf16_t* op = out + (((int64_t)b * S + qrow) * Hq + hq) * kHeadDim;
@@ -471,7 +603,7 @@ int attn_prefill(const void* q, const void* k_cache, const void* v_cache, const 
     hipStream_t st = (hipStream_t)stream;
     if (dtype == CRANE_HIP_BF16) {
         // candle scales the bf16 scores by the scale converted to bf16 (affine in T)
-        const float sl = host_round_bf16(scale) * kLog2e;
+        const uint32_t sl = f32_bits(host_round_bf16(scale)) >> 16;
         const int n_rep = Hq / Hkv;
         const int64_t n_qt = (S + kBM - 1) / kBM;
         const int64_t units = n_qt * B * Hkv;

@@ -52,6 +52,10 @@ class DecoderLayer:
                 w.gate_up.shape != (2 * self.inter, self.hidden) or w.down.shape != (self.hidden, self.inter):
             raise CraneHipError(E_INVALID, "layer weight shapes do not match the head counts and sizes")
         self.cache = KvCache(batch, num_kv_heads, dtype=w.qkv.dtype, device=w.qkv.device)
+        # Decode scores follow the candle path the model takes: Qwen2.5
+        # (rope only, candle-transformers qwen2) always the standard SDPA;
+        # Qwen3 and Hunyuan the grouped one when n_rep > 1.
+        self.score_mode = "standard" if order == "rope_only" else None
 
     def forward(self, x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, positions: torch.Tensor) -> torch.Tensor:
         """x [B, S, hidden]; positions [B] int32, the rope position of each
@@ -66,7 +70,7 @@ class DecoderLayer:
         q = self.cache.append_qkv(qkv, cos, sin, positions, self.num_heads, w.q_norm, w.k_norm, self.eps,
                                   self.order)
         if S == 1:
-            attn = self.cache.decode(q.view(B, self.num_heads, ops.HEAD_DIM))
+            attn = self.cache.decode(q.view(B, self.num_heads, ops.HEAD_DIM), score_mode=self.score_mode)
         else:
             attn = self.cache.prefill(q)
         o = ops.linear(attn.view(B * S, -1), w.o)

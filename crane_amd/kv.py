@@ -168,9 +168,10 @@ class KvCache:
         return q_out
 
     def decode(self, q: torch.Tensor, scale: Optional[float] = None,
-               workspace: Optional[torch.Tensor] = None) -> torch.Tensor:
-        """Decode attention of q [B, Hq, D] over every sequence's rows; [B, 1, Hq*D]."""
-        from .ops import decode_workspace
+               workspace: Optional[torch.Tensor] = None, score_mode: Optional[str] = None) -> torch.Tensor:
+        """Decode attention of q [B, Hq, D] over every sequence's rows; [B, 1, Hq*D]
+        (score_mode as in ops.attention_decode)."""
+        from .ops import decode_workspace, score_mode_code
         _check_q(q, 3, self.batch, self.dtype, self.device)
         q = q.contiguous()
         B, Hq, D = q.shape
@@ -180,7 +181,8 @@ class KvCache:
             _dev(q, workspace)
         ws = workspace if workspace is not None else decode_workspace(q.device, need)
         out = torch.empty((B, 1, Hq * D), dtype=q.dtype, device=q.device)
-        check(_lib.lib().crane_kv_decode(self._h, q.data_ptr(), Hq, scale if scale else D ** -0.5, ws.data_ptr(),
+        check(_lib.lib().crane_kv_decode(self._h, q.data_ptr(), Hq, scale if scale else D ** -0.5,
+                                         score_mode_code(score_mode, Hq // self.num_kv_heads), ws.data_ptr(),
                                          ws.numel() * ws.element_size(), out.data_ptr(), _stream(q.device)),
               "crane_kv_decode")
         return out
@@ -333,9 +335,10 @@ class PagedKvCache:
         return q_out
 
     def decode(self, q: torch.Tensor, scale: Optional[float] = None,
-               workspace: Optional[torch.Tensor] = None) -> torch.Tensor:
-        """Decode attention of q [B, Hq, D] over the batch's rows; [B, 1, Hq*D]."""
-        from .ops import decode_workspace
+               workspace: Optional[torch.Tensor] = None, score_mode: Optional[str] = None) -> torch.Tensor:
+        """Decode attention of q [B, Hq, D] over the batch's rows; [B, 1, Hq*D]
+        (score_mode as in ops.attention_decode)."""
+        from .ops import decode_workspace, score_mode_code
         _check_q(q, 3, len(self._batch), self.dtype, self.device)
         q = q.contiguous()
         B, Hq, D = q.shape
@@ -345,7 +348,8 @@ class PagedKvCache:
             _dev(q, workspace)
         ws = workspace if workspace is not None else decode_workspace(q.device, need)
         out = torch.empty((B, 1, Hq * D), dtype=q.dtype, device=q.device)
-        check(_lib.lib().crane_pkv_decode(self._h, q.data_ptr(), Hq, scale if scale else D ** -0.5, ws.data_ptr(),
+        check(_lib.lib().crane_pkv_decode(self._h, q.data_ptr(), Hq, scale if scale else D ** -0.5,
+                                          score_mode_code(score_mode, Hq // self.num_kv_heads), ws.data_ptr(),
                                           ws.numel() * ws.element_size(), out.data_ptr(), _stream(q.device)),
               "crane_pkv_decode")
         return out

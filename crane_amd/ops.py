@@ -23,7 +23,22 @@ from ._lib import CraneHipError, check
 _DTYPES = {torch.float32: _lib.F32, torch.bfloat16: _lib.BF16}
 _ORDERS = {"norm_then_rope": _lib.NORM_THEN_ROPE, "rope_then_norm": _lib.ROPE_THEN_NORM,
            "rope_only": _lib.ROPE_ONLY}
+_SCORES = {"grouped": _lib.SCORE_GROUPED, "standard": _lib.SCORE_STANDARD}
 HEAD_DIM = 128
+
+
+def score_mode_code(score_mode: Optional[str], n_rep: int) -> int:
+    """The candle SDPA form a decode call reproduces.  None picks the one
+    Qwen3 and Hunyuan take (qwen3/modeling.rs:432 `n_rep > 1 && seq_len == 1`:
+    the grouped path, q pre-scaled; otherwise the standard path, scores
+    post-scaled); Qwen2.5 (candle-transformers qwen2, qwen25/qwen2.rs:196-197)
+    always takes "standard"."""
+    if score_mode is None:
+        return _lib.SCORE_GROUPED if n_rep > 1 else _lib.SCORE_STANDARD
+    try:
+        return _SCORES[score_mode]
+    except KeyError:
+        raise CraneHipError(_lib.E_INVALID, f"score_mode {score_mode!r}") from None
 
 
 def _dtype_code(t: torch.Tensor) -> int:
@@ -67,38 +82,37 @@ def _ptr(t: Optional[torch.Tensor]) -> Optional[int]:
 
 # ---------------------------------------------------------------- rope tables
 
+def _host_tables(fn, args, head_dim: int, max_pos: int, device, dtype: torch.dtype):
+    code = _dtype_code(torch.empty(0, dtype=dtype))
+    cos = torch.empty((max_pos, head_dim // 2), dtype=dtype)
+    sin = torch.empty_like(cos)
+    check(fn(head_dim, *args, max_pos, code, cos.data_ptr(), sin.data_ptr()), fn.__name__)
+    return cos.to(device), sin.to(device)
+
+
 def rope_tables(head_dim: int, theta: float, max_pos: int, alpha: float = 0.0,
                 device: torch.device | str = "cuda", dtype: torch.dtype = torch.float32):
-    """cos/sin tables [max_pos, head_dim/2] following qwen3/modeling.rs:117-139
-    (inv_freq = 1.0f32 / (f32)(base^(2i/d)) with the power in f64; f32 products;
-    cos/sin in f32) and the Hunyuan NTK-alpha base of
-    hunyuan_dense/modeling.rs:202-219, then cast to the model dtype as
-    qwen3/modeling.rs:857-864 does.  Built once per model, like the reference."""
-    base = float(theta)
-    if alpha and alpha > 0.0:
-        base = theta * alpha ** (head_dim / (head_dim - 2.0))
-    # f64 power, cast to f32, then an f32 reciprocal
-    powers = torch.tensor([base ** (i / head_dim) for i in range(0, head_dim, 2)], dtype=torch.float64)
-    inv = torch.ones((), dtype=torch.float32) / powers.to(torch.float32)
-    pos = torch.arange(max_pos, dtype=torch.float32)
-    freqs = (pos[:, None] * inv[None, :]).to(device)
-    return freqs.cos().to(dtype).contiguous(), freqs.sin().to(dtype).contiguous()
+    """cos/sin tables [max_pos, head_dim/2] in the model dtype, bit-identical to
+    Crane's: qwen3/modeling.rs:117-139 (inv_freq = 1.0f32 / (f32)(base^(2i/d))
+    with the power in f64, f32 products, f32 cos/sin) with the Hunyuan
+    NTK-alpha base of hunyuan_dense/modeling.rs:202-219 when alpha > 0, cast to
+    the model dtype as qwen3/modeling.rs:857-864 does.  Built on the host by
+    crane_hip_rope_tables (the C library's cosf/sinf, which Rust's f32::cos and
+    f32::sin call) once per model, then copied to `device`."""
+    return _host_tables(_lib.lib().crane_hip_rope_tables, (float(theta), float(alpha or 0.0)), head_dim, max_pos,
+                        device, dtype)
 
 
 def rope_tables_qwen2(head_dim: int, theta: float, max_pos: int, device: torch.device | str = "cuda",
                       dtype: torch.dtype = torch.float32):
     """cos/sin tables [max_pos, head_dim/2] in candle-transformers qwen2's form
-    (copy at qwen25/qwen2.rs:47-64): inv_freq = 1 / theta^(2i/d) (f32) and the
-    positions are cast to the model dtype before the k=1 product, whose result
-    is rounded to the model dtype, and cos/sin are computed in f32 and rounded.
-    In bf16 this rounds positions above 256 and the angles themselves; in f32
-    it equals rope_tables.  Built on the host once per model."""
-    powers = torch.tensor([float(theta) ** (i / head_dim) for i in range(0, head_dim, 2)], dtype=torch.float64)
-    inv = (torch.ones((), dtype=torch.float32) / powers.to(torch.float32)).to(dtype)
-    pos = torch.arange(max_pos, dtype=torch.float32).to(dtype)
-    # a product of two bf16 values is exact in f32, so this is the one rounding of candle's matmul
-    freqs = (pos.float()[:, None] * inv.float()[None, :]).to(dtype).float()
-    return (freqs.cos().to(dtype).contiguous().to(device), freqs.sin().to(dtype).contiguous().to(device))
+    (copy at qwen25/qwen2.rs:47-64): inv_freq and the positions are cast to the
+    model dtype before the k=1 product, whose result is rounded to the model
+    dtype, and cos/sin are computed in f32 and rounded.  In bf16 this rounds
+    positions above 256 and the angles themselves; in f32 it equals
+    rope_tables.  Built on the host (crane_hip_rope_tables_qwen2) once per
+    model, then copied to `device`."""
+    return _host_tables(_lib.lib().crane_hip_rope_tables_qwen2, (float(theta),), head_dim, max_pos, device, dtype)
 
 
 # ------------------------------------------------------------ fused append op
@@ -212,12 +226,13 @@ def decode_workspace(device: torch.device, nbytes: int) -> torch.Tensor:
 
 def attention_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
                      kv_len: torch.Tensor, max_kv: int, scale: Optional[float] = None,
-                     workspace: Optional[torch.Tensor] = None) -> torch.Tensor:
+                     workspace: Optional[torch.Tensor] = None, score_mode: Optional[str] = None) -> torch.Tensor:
     """Batched decode attention, one new token per sequence: q [B, Hq, D] (or
     [B, Hq, 1, D]) over cache rows [0, kv_len[b]).  Returns [B, 1, Hq*D].
 
-    Replaces the GQA-grouped decode SDPA of qwen3/modeling.rs:432-467 and the
-    pad + mask of the batched path (:1118-1200)."""
+    Replaces the GQA-grouped decode SDPA of qwen3/modeling.rs:432-467 (or, with
+    score_mode "standard", the standard SDPA of :485-500 / qwen2.rs:196-201;
+    see score_mode_code) and the pad + mask of the batched path (:1118-1200)."""
     dev = _dev(q, k_cache, v_cache, kv_len, workspace)
     if q.dim() == 4:
         if q.shape[2] != 1:
@@ -240,9 +255,10 @@ def attention_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tens
     if workspace is None:
         workspace = decode_workspace(dev, need)
     out = torch.empty((B, 1, Hq * D), dtype=q.dtype, device=dev)
+    mode = score_mode_code(score_mode, Hq // Hkv)
     rc = _lib.lib().crane_hip_attn_decode(
         q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), k_cache.shape[2], kv_len.data_ptr(),
-        max_kv, B, Hq, Hkv, D, scale, workspace.data_ptr(), workspace.numel() * workspace.element_size(),
+        max_kv, B, Hq, Hkv, D, scale, mode, workspace.data_ptr(), workspace.numel() * workspace.element_size(),
         out.data_ptr(), dt, _stream(dev))
     check(rc, "attention_decode")
     return out
@@ -329,7 +345,7 @@ def qk_norm_rope_append_paged(qkv: torch.Tensor, cos: torch.Tensor, sin: torch.T
 
 def attention_decode_paged(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tensor, block_table: torch.Tensor,
                            kv_len: torch.Tensor, max_kv: int, scale: Optional[float] = None,
-                           workspace: Optional[torch.Tensor] = None) -> torch.Tensor:
+                           workspace: Optional[torch.Tensor] = None, score_mode: Optional[str] = None) -> torch.Tensor:
     """attention_decode over a paged cache: q [B, Hq, D]; [B, 1, Hq*D]."""
     dev = _dev(q, k_pool, v_pool, block_table, kv_len, workspace)
     if q.dim() != 3 or q.shape[2] != HEAD_DIM:
@@ -345,7 +361,7 @@ def attention_decode_paged(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.
     out = torch.empty((B, 1, Hq * D), dtype=q.dtype, device=dev)
     rc = _lib.lib().crane_hip_attn_decode_paged(
         q.data_ptr(), k_pool.data_ptr(), v_pool.data_ptr(), n_pages, page_rows, block_table.data_ptr(), stride,
-        kv_len.data_ptr(), max_kv, B, Hq, Hkv, D, scale, workspace.data_ptr(),
+        kv_len.data_ptr(), max_kv, B, Hq, Hkv, D, scale, score_mode_code(score_mode, Hq // Hkv), workspace.data_ptr(),
         workspace.numel() * workspace.element_size(), out.data_ptr(), dt, _stream(dev))
     check(rc, "attention_decode_paged")
     return out

@@ -43,7 +43,7 @@
 extern "C" {
 #endif
 
-#define CRANE_HIP_ABI_VERSION 1
+#define CRANE_HIP_ABI_VERSION 2
 
 enum crane_hip_dtype { CRANE_HIP_F32 = 0, CRANE_HIP_BF16 = 1 };
 
@@ -55,6 +55,19 @@ enum crane_hip_order {
     CRANE_HIP_ROPE_THEN_NORM = 1,
     CRANE_HIP_ROPE_ONLY = 2
 };
+
+/* Which of candle's two SDPA forms the decode scores follow (the scores'
+ * rounding points differ in the model dtype).  Crane picks the form per call:
+ *   GROUPED  -- the GQA-grouped decode of qwen3/modeling.rs:432-467 and
+ *               hunyuan_dense/modeling.rs:575-608, taken when n_rep > 1 and
+ *               seq_len == 1: q * scale rounded to T (:440-441), then q@K^T
+ *               rounded to T;
+ *   STANDARD -- the standard SDPA of qwen3/modeling.rs:485-488 (taken for
+ *               n_rep == 1), hunyuan_dense/modeling.rs:628-631, and every decode
+ *               of candle-transformers qwen2 (qwen25/qwen2.rs:196-197): q@K^T
+ *               rounded to T, then * scale rounded to T.
+ * In f32 both forms differ only in the last bits of the scores. */
+enum crane_hip_score { CRANE_HIP_SCORE_GROUPED = 0, CRANE_HIP_SCORE_STANDARD = 1 };
 
 enum crane_hip_status {
     CRANE_HIP_OK = 0,
@@ -112,6 +125,26 @@ int crane_hip_qnorm_rope(const void* q, int64_t q_row_stride, const void* q_norm
                          const int32_t* positions, void* q_out, int B, int S, int Hq, int D, int dtype,
                          void* stream);
 
+/* RoPE cos/sin tables [max_pos, dim/2] in `dtype`, built on the host CPU into
+ * caller-provided HOST memory (upload them once per model).  Bit-identical to
+ * Crane's tables:
+ *   qwen3/modeling.rs:117-139 (RotaryEmbedding::new: inv_freq = 1.0f32 /
+ *   (f32)(base^(2i/dim)) with the power in f64, f32 products p * inv_freq, f32
+ *   cosf/sinf) and :857-864 (the tables cast to the model dtype); alpha > 0
+ *   gives Hunyuan's NTK-alpha base theta * alpha^(dim/(dim-2))
+ *   (hunyuan_dense/modeling.rs:202-219); alpha = 0 leaves theta as the base.
+ * Returns CRANE_HIP_E_INVALID for dim odd or above 1024, max_pos < 0, a null
+ * table or a non-positive theta. */
+int crane_hip_rope_tables(int dim, double theta, double alpha, int64_t max_pos, int dtype, void* cos_out,
+                          void* sin_out);
+
+/* The tables of candle-transformers qwen2 (copy at qwen25/qwen2.rs:47-64):
+ * inv_freq and the positions are cast to the model dtype before the product,
+ * which is rounded to it; cos/sin are computed in f32 and rounded to it.  In
+ * bf16 this rounds positions above 256.  In f32 it equals
+ * crane_hip_rope_tables(dim, theta, 0, ...). */
+int crane_hip_rope_tables_qwen2(int dim, double theta, int64_t max_pos, int dtype, void* cos_out, void* sin_out);
+
 /* Bytes of workspace crane_hip_attn_decode needs for these sizes (max_kv is
  * the largest kv_len the call may see). */
 size_t crane_hip_attn_decode_workspace(int B, int Hq, int Hkv, int D, int64_t max_kv, int dtype);
@@ -124,14 +157,19 @@ size_t crane_hip_attn_decode_workspace(int B, int Hq, int Hkv, int D, int64_t ma
  *          included); 1 <= kv_len[b] <= max_kv <= cache_cap.  A sequence with
  *          kv_len[b] == 0 gets an all-zero output row.
  * scale    softmax scale (1/sqrt(D) in every supported model)
+ * score_mode CRANE_HIP_SCORE_GROUPED or CRANE_HIP_SCORE_STANDARD: the candle SDPA
+ *          form whose score rounding the call reproduces (see crane_hip_score)
  * out      [B, 1, Hq*D]
  * workspace device scratch of at least crane_hip_attn_decode_workspace(...) bytes,
  *          16-byte aligned, any contents (partial results of the split-KV pass);
  *          calls that overlap in time must not share a workspace.
+ * A sequence of at most 256 keys (512 when max_kv > 12288) gets candle's
+ * softmax_last_dim chain in the model dtype; longer ones are split over key
+ * chunks whose partial results are merged by their log-sum-exp.
  * Replaces: qwen3/modeling.rs:432-467 and :1118-1200 (see the file header). */
 int crane_hip_attn_decode(const void* q, const void* k_cache, const void* v_cache,
                           int64_t cache_cap, const int32_t* kv_len, int64_t max_kv, int B,
-                          int Hq, int Hkv, int D, float scale, void* workspace,
+                          int Hq, int Hkv, int D, float scale, int score_mode, void* workspace,
                           size_t ws_bytes, void* out, int dtype, void* stream);
 
 /* Causal (or full) GQA prefill attention over the cache.
@@ -188,7 +226,7 @@ int crane_hip_qknorm_rope_append_paged(const void* qkv, int64_t qkv_row_stride,
 int crane_hip_attn_decode_paged(const void* q, const void* k_pool, const void* v_pool,
                                 int64_t n_pages, int page_rows, const int32_t* block_table,
                                 int64_t table_stride, const int32_t* kv_len, int64_t max_kv, int B,
-                                int Hq, int Hkv, int D, float scale, void* workspace,
+                                int Hq, int Hkv, int D, float scale, int score_mode, void* workspace,
                                 size_t ws_bytes, void* out, int dtype, void* stream);
 
 /* crane_hip_attn_prefill over the pools (max_start + S <= table_stride * page_rows). */

@@ -74,9 +74,10 @@ int crane_kv_append_qkv(crane_kv* kv, const void* qkv, int64_t qkv_row_stride, c
                         int64_t cs_stride, int64_t table_rows, const int32_t* positions, void* q_out, int S,
                         int Hq, void* stream);
 
-/* Decode over the cache (crane_hip_attn_decode with kv_len = the lengths). */
-int crane_kv_decode(const crane_kv* kv, const void* q, int Hq, float scale, void* workspace, size_t ws_bytes,
-                    void* out, void* stream);
+/* Decode over the cache (crane_hip_attn_decode with kv_len = the lengths;
+ * score_mode as there). */
+int crane_kv_decode(const crane_kv* kv, const void* q, int Hq, float scale, int score_mode, void* workspace,
+                    size_t ws_bytes, void* out, void* stream);
 
 /* Causal or full prefill of the last S rows of every sequence (queries q
  * [B, Hq, S, D]; sequence b's chunk starts at row len[b] - S). */
@@ -97,7 +98,8 @@ uint64_t crane_kv_bytes(const crane_kv* kv);
 
 /* Batched decode set-up: `dst` (B = n, same Hkv, D, dtype; any prior buffer is
  * released) receives a buffer of max_i(len_i) + extra_room rows and the rows
- * of srcs[i] (each B = 1) at rows [0, len_i) of sequence i. */
+ * of srcs[i] (each B = 1) at rows [0, len_i) of sequence i.  No srcs[i] may be
+ * dst itself (CRANE_HIP_E_INVALID: its rows would be released first). */
 int crane_kv_stack(crane_kv* dst, const crane_kv* const* srcs, int n, int64_t extra_room, void* stream);
 
 /* Batched decode tear-down: copy sequence i of `batch` (its len_i rows) into

@@ -75,9 +75,10 @@ int crane_pkv_append_qkv(crane_pkv* pkv, const void* qkv, int64_t qkv_row_stride
                          int64_t cs_stride, int64_t table_rows, const int32_t* positions, void* q_out, int S,
                          int Hq, void* stream);
 
-/* Decode over the batch's rows (crane_hip_attn_decode_paged, kv_len = the lengths). */
-int crane_pkv_decode(const crane_pkv* pkv, const void* q, int Hq, float scale, void* workspace, size_t ws_bytes,
-                     void* out, void* stream);
+/* Decode over the batch's rows (crane_hip_attn_decode_paged, kv_len = the
+ * lengths; score_mode as there). */
+int crane_pkv_decode(const crane_pkv* pkv, const void* q, int Hq, float scale, int score_mode, void* workspace,
+                     size_t ws_bytes, void* out, void* stream);
 
 /* Causal or full prefill of the last S rows of every batch sequence (queries
  * q [B, Hq, S, D]; sequence b's chunk starts at row len[b] - S). */

@@ -38,6 +38,14 @@ def scale() -> float:
     return 1.0 / math.sqrt(D)
 
 
+def decode_variant(orc, Hq: int, Hkv: int, score_mode=None) -> int:
+    """The oracle decode form matching a kernel call's score mode (None: the
+    rule of qwen3/modeling.rs:432, grouped iff n_rep > 1)."""
+    if score_mode is None:
+        score_mode = "grouped" if Hq // Hkv > 1 else "standard"
+    return orc.DECODE_GROUPED if score_mode == "grouped" else orc.DECODE_STANDARD
+
+
 def decode_case(seed, B, Hq, Hkv, lens, cap=None, dtype="bf16", std=1.0, poison=True):
     """q [B,Hq,D], K/V caches [B,Hkv,cap,D] with rows >= lens[b] set to NaN
     (a kernel that reads past kv_len produces NaN)."""

@@ -44,7 +44,7 @@ def test_library_exports_every_declared_symbol():
 
 
 def test_strerror_and_version():
-    assert _lib.version().startswith("crane_hip 1 gfx950")
+    assert _lib.version().startswith("crane_hip 2 gfx950")
     for code in range(0, 9):
         assert _lib.strerror(code)
     assert "capacity" in _lib.strerror(_lib.E_CAPACITY)
@@ -53,11 +53,11 @@ def test_strerror_and_version():
 
 def _decode(**kw):
     a = dict(q=16, k=16, v=16, cap=4096, kv_len=16, max_kv=4096, B=1, Hq=32, Hkv=8, D=128, scale=0.088,
-             ws=16, ws_bytes=1 << 30, out=16, dtype=1, stream=None)
+             score=_lib.SCORE_GROUPED, ws=16, ws_bytes=1 << 30, out=16, dtype=1, stream=None)
     a.update(kw)
     return _lib.lib().crane_hip_attn_decode(a["q"], a["k"], a["v"], a["cap"], a["kv_len"], a["max_kv"], a["B"],
-                                            a["Hq"], a["Hkv"], a["D"], a["scale"], a["ws"], a["ws_bytes"],
-                                            a["out"], a["dtype"], a["stream"])
+                                            a["Hq"], a["Hkv"], a["D"], a["scale"], a["score"], a["ws"],
+                                            a["ws_bytes"], a["out"], a["dtype"], a["stream"])
 
 
 @pytest.mark.parametrize("kw,code", [
@@ -67,6 +67,8 @@ def _decode(**kw):
     (dict(max_kv=5000), _lib.E_CAPACITY),
     (dict(max_kv=0), _lib.E_INVALID),
     (dict(scale=0.0), _lib.E_INVALID),
+    (dict(score=2), _lib.E_INVALID),
+    (dict(score=-1), _lib.E_INVALID),
     (dict(q=None), _lib.E_INVALID),
     (dict(q=8), _lib.E_ALIGN),
     (dict(ws_bytes=100), _lib.E_WORKSPACE),
@@ -79,14 +81,17 @@ def test_decode_argument_checks(kw, code):
 
 @pytest.mark.parametrize("B,Hq,Hkv,max_kv", [(32, 32, 8, 4097), (8, 64, 8, 32769), (1, 16, 8, 1025)])
 def test_decode_workspace_size(B, Hq, Hkv, max_kv):
-    """[B, Hq, splits, D] f32 partial rows, then [B, Hq, splits, 2] f32 (max, sum)
-    pairs; one split per 256 keys."""
+    """[B, Hq, splits, D] partial rows in the call's dtype (bf16 rows for bf16
+    calls, f32 for f32), then [B, Hq, splits, 2] f32 (max, sum) pairs; one split
+    per 256 keys."""
     L = _lib.lib()
     ns = (max_kv + 255) // 256
     up = lambda x: (x + 255) // 256 * 256
-    assert L.crane_hip_attn_decode_workspace(B, Hq, Hkv, 128, max_kv, 1) == up(B * Hq * ns * 128 * 4) + up(B * Hq * ns * 8)
+    assert L.crane_hip_attn_decode_workspace(B, Hq, Hkv, 128, max_kv, 1) == up(B * Hq * ns * 128 * 2) + up(B * Hq * ns * 8)
+    assert L.crane_hip_attn_decode_workspace(B, Hq, Hkv, 128, max_kv, 0) == up(B * Hq * ns * 128 * 4) + up(B * Hq * ns * 8)
     assert L.crane_hip_attn_decode_workspace(32, 32, 8, 64, 4096, 1) == 0
     assert L.crane_hip_attn_decode_workspace(0, 32, 8, 128, 4096, 1) == 0
+    assert L.crane_hip_attn_decode_workspace(32, 32, 8, 128, 4096, 7) == 0
 
 
 def _prefill(**kw):
@@ -179,3 +184,19 @@ def test_ops_reject_cpu_tensors():
     k = torch.zeros(1, 2, 16, 128, dtype=torch.bfloat16)
     with pytest.raises(_lib.CraneHipError, match="GPU only"):
         ops.attention_decode(q, k, k, torch.ones(1, dtype=torch.int32), 16)
+
+
+def test_kv_stack_and_extract_reject_aliasing():
+    """A batch cache cannot be its own source (crane_kv_stack releases dst's
+    buffer before copying) or its own extraction target; both are rejected on
+    the host before any device call."""
+    L = _lib.lib()
+    h = ctypes.c_void_p()
+    assert L.crane_kv_create(1, 8, 128, _lib.BF16, ctypes.byref(h)) == _lib.OK
+    try:
+        srcs = (ctypes.c_void_p * 1)(h.value)
+        assert L.crane_kv_stack(h, srcs, 1, 0, None) == _lib.E_INVALID
+        assert L.crane_kv_extract(h, 0, h, None) == _lib.E_INVALID
+        assert L.crane_kv_stack(h, None, 1, 0, None) == _lib.E_INVALID
+    finally:
+        L.crane_kv_destroy(h)

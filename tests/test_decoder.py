@@ -65,7 +65,10 @@ class RefLayer:
                                   w["q_norm"], w["k_norm"], eps, self.order, "bf16")
         scale = 1 / math.sqrt(D)
         if S == 1:
-            a = o.attn_decode(q[:, :, 0], self.kc, self.vc, self.len + 1, scale, "bf16")
+            # Qwen2.5 (rope only) decodes by the standard SDPA; Qwen3 / Hunyuan by the grouped one
+            mode = "standard" if self.order == 2 else None
+            a = o.attn_decode(q[:, :, 0], self.kc, self.vc, self.len + 1, scale, "bf16",
+                              cases.decode_variant(o, self.Hq, self.Hkv, mode))
         else:
             a = o.attn_prefill(q, self.kc, self.vc, self.len, scale, True, "bf16")
         self.len = self.len + S

@@ -41,33 +41,36 @@ def note(msg):
 # ------------------------------------------------------------------ decode
 
 DECODE_CASES = [
-    # name, B, Hq, Hkv, lens, dtype, std
-    ("c1_qwen3_0.6b_f32", 1, 16, 8, [1025], "f32", 1.0),
-    ("c3_qwen3_8b_bf16", 32, 32, 8, None, "bf16", 1.0),
-    ("ragged_edges_bf16", 6, 8, 2, [1, 255, 256, 257, 511, 1000], "bf16", 1.0),
-    ("ragged_edges_f32", 5, 8, 2, [1, 2, 256, 257, 700], "f32", 1.0),
-    ("mha_nrep1_bf16", 3, 4, 4, [17, 300, 64], "bf16", 1.0),
-    ("qwen25_7b_gqa7_bf16", 4, 28, 4, [100, 1500, 4096, 33], "bf16", 1.0),
-    ("gqa16_bf16", 2, 32, 2, [513, 2000], "bf16", 1.0),
-    ("gqa3_f32", 2, 6, 2, [40, 900], "f32", 1.0),
-    # max_kv past 12288: 512-key chunks and the 4-partition merge
-    ("long_chunks_f32", 2, 8, 2, [13000, 20001], "f32", 1.0),
-    ("long_chunks_ragged_bf16", 3, 16, 2, [12289, 15000, 700], "bf16", 1.0),
+    # name, B, Hq, Hkv, lens, dtype, std, score mode (None: Qwen3/Hunyuan's rule, grouped iff n_rep > 1)
+    ("c1_qwen3_0.6b_f32", 1, 16, 8, [1025], "f32", 1.0, None),
+    ("c3_qwen3_8b_bf16", 32, 32, 8, None, "bf16", 1.0, None),
+    ("ragged_edges_bf16", 6, 8, 2, [1, 255, 256, 257, 511, 1000], "bf16", 1.0, None),
+    ("ragged_edges_f32", 5, 8, 2, [1, 2, 256, 257, 700], "f32", 1.0, None),
+    ("mha_nrep1_bf16", 3, 4, 4, [17, 300, 64], "bf16", 1.0, None),
+    ("mha_nrep1_f32", 2, 4, 4, [200, 700], "f32", 1.0, None),
+    # Qwen2.5 (candle-transformers qwen2): always the standard SDPA
+    ("qwen25_7b_gqa7_bf16", 4, 28, 4, [100, 1500, 4096, 33], "bf16", 1.0, "standard"),
+    ("qwen25_ragged_standard_bf16", 6, 8, 2, [1, 255, 256, 257, 511, 1000], "bf16", 1.0, "standard"),
+    ("gqa16_bf16", 2, 32, 2, [513, 2000], "bf16", 1.0, None),
+    ("gqa3_f32", 2, 6, 2, [40, 900], "f32", 1.0, None),
+    # max_kv past 12288: 512-key chunks and the 8-partition merge
+    ("long_chunks_f32", 2, 8, 2, [13000, 20001], "f32", 1.0, None),
+    ("long_chunks_ragged_bf16", 3, 16, 2, [12289, 15000, 700], "bf16", 1.0, None),
 ]
 
 
-@pytest.mark.parametrize("name,B,Hq,Hkv,lens,dtype,std", DECODE_CASES, ids=[c[0] for c in DECODE_CASES])
-def test_decode_parity(gpu, orc, name, B, Hq, Hkv, lens, dtype, std):
+@pytest.mark.parametrize("name,B,Hq,Hkv,lens,dtype,std,mode", DECODE_CASES, ids=[c[0] for c in DECODE_CASES])
+def test_decode_parity(gpu, orc, name, B, Hq, Hkv, lens, dtype, std, mode):
     from crane_amd import ops
     if lens is None:
         lens = cases.c3_lengths()
-    note(f"decode {name}: B={B} Hq={Hq} Hkv={Hkv} dtype={dtype} max_len={max(lens)}")
+    note(f"decode {name}: B={B} Hq={Hq} Hkv={Hkv} dtype={dtype} max_len={max(lens)} mode={mode}")
     q, k, v, lens = cases.decode_case(cases.SEED0 + zlib.crc32(name.encode()) % 1000, B, Hq, Hkv, lens, dtype=dtype, std=std)
     cap = k.shape[2]
     out = ops.attention_decode(dev_t(q, dtype, gpu), dev_t(k, dtype, gpu), dev_t(v, dtype, gpu), i32(lens, gpu),
-                               int(lens.max()), cases.scale())
+                               int(lens.max()), cases.scale(), score_mode=mode)
     torch.cuda.synchronize()
-    ref = orc.attn_decode(q, k, v, lens, cases.scale(), dtype)
+    ref = orc.attn_decode(q, k, v, lens, cases.scale(), dtype, cases.decode_variant(orc, Hq, Hkv, mode))
     note(f"  errors vs oracle: max-abs {errors(host(out).reshape(B, Hq * D), ref)}")
     assert_close(host(out).reshape(B, Hq * D), ref, dtype, name)
     assert cap == int(lens.max())
@@ -82,7 +85,7 @@ def test_decode_c5_long_context(gpu, orc):
     q, k, v, lens = cases.decode_case(cases.SEED0 + 5, B, Hq, Hkv, [L, L], dtype="bf16",
                                       std=math.sqrt(0.5), poison=False)
     out = ops.attention_decode(dev_t(q, "bf16", gpu), dev_t(k, "bf16", gpu), dev_t(v, "bf16", gpu),
-                               i32(lens, gpu), L)
+                               i32(lens, gpu), L, score_mode="standard")
     ref = orc.attn_decode(q, k, v, lens, cases.scale(), "bf16", orc.DECODE_STANDARD)
     assert_close(host(out).reshape(B, Hq * D), ref, "bf16", "c5")
 

@@ -36,8 +36,9 @@ def test_rope_tables_closed_form(orc):
     assert np.all(np.abs(sin - ref_s) <= ulp + 1e-45)
     assert np.all(cos[0] == 1.0) and np.all(sin[0] == 0.0)      # identity row
     assert cos[1, 0] == np.float32(math.cos(1.0)) or abs(cos[1, 0] - math.cos(1.0)) < 1e-7
-    # frequencies decrease along the row: the last pair rotates slowest
-    assert abs(sin[1000, -1]) < abs(sin[1000, 1]) or True
+    # frequencies decrease along the row: at position 1 every angle inv[k] is
+    # below pi/2, so sin falls strictly and cos rises (to 1 in f32) pair by pair
+    assert np.all(np.diff(sin[1]) < 0) and np.all(np.diff(cos[1]) >= 0) and cos[1, -1] > cos[1, 0]
     assert inv[0] == 1.0 and inv[-1] < inv[1] < inv[0]
 
 
@@ -71,23 +72,49 @@ def test_rope_tables_qwen2_dtype(orc):
 
 
 def test_rope_tables_qwen2_host_builder(orc):
-    """ops.rope_tables_qwen2 (the tables a Qwen2.5 model hands the append)
-    against the oracle's qwen2 chain: bf16 within one bf16 ulp and almost all
-    equal (the host cos may differ from glibc's in the last f32 bit before the
-    rounding), f32 within one f32 ulp."""
+    """ops.rope_tables_qwen2 (the tables a Qwen2.5 model hands the append,
+    built by the library's crane_hip_rope_tables_qwen2 on the host) equals the
+    oracle's qwen2 chain bit for bit, in bf16 and f32."""
     import torch
     from crane_amd import ops
     cb, sb = orc.rope_tables_qwen2(D, 1e6, 3000, "bf16")
     tc, ts = ops.rope_tables_qwen2(D, 1e6, 3000, device="cpu", dtype=torch.bfloat16)
-    for got, ref in ((tc.float().numpy(), cb), (ts.float().numpy(), sb)):
-        assert np.max(np.abs(got - ref)) <= 2 ** -8
-        assert np.mean(got == ref) > 0.999
+    assert np.array_equal(tc.float().numpy(), cb) and np.array_equal(ts.float().numpy(), sb)
     assert torch.equal(tc[256], tc[257])                       # positions rounded to bf16
     cf, sf = orc.rope_tables_qwen2(D, 1e6, 3000, "f32")
     tc, ts = ops.rope_tables_qwen2(D, 1e6, 3000, device="cpu", dtype=torch.float32)
-    for got, ref in ((tc.numpy(), cf), (ts.numpy(), sf)):
-        ulp = np.spacing(np.abs(ref)).astype(np.float64)
-        assert np.all(np.abs(got.astype(np.float64) - ref) <= ulp + 1e-45)
+    assert np.array_equal(tc.numpy(), cf) and np.array_equal(ts.numpy(), sf)
+
+
+@pytest.mark.parametrize("theta,alpha,max_pos", [(1e6, 0.0, 40000), (1e4, 0.0, 5000), (1e4, 1000.0, 5000),
+                                                 (1e6, 2.5, 33000)])
+def test_rope_tables_host_builder(orc, theta, alpha, max_pos):
+    """ops.rope_tables (the tables the fused append reads: qwen3/modeling.rs:
+    117-139 cast to the model dtype as :857-864 does, and Hunyuan's NTK-alpha
+    base) equals the oracle bit for bit: f32 tables, and bf16 tables equal to
+    the oracle's f32 tables rounded to nearest even.  Positions up to c5's
+    32769 rows are covered."""
+    import torch
+    from crane_amd import ops
+    c, s = orc.rope_tables(D, theta, max_pos, alpha=alpha)
+    tc, ts = ops.rope_tables(D, theta, max_pos, alpha=alpha, device="cpu", dtype=torch.float32)
+    assert np.array_equal(tc.numpy(), c) and np.array_equal(ts.numpy(), s)
+    bc, bs = ops.rope_tables(D, theta, max_pos, alpha=alpha, device="cpu", dtype=torch.bfloat16)
+    assert np.array_equal(bc.float().numpy(), orc.round_bf16(c)) and np.array_equal(bs.float().numpy(), orc.round_bf16(s))
+
+
+def test_rope_table_builder_argument_checks():
+    import ctypes
+    from crane_amd import _lib
+    L = _lib.lib()
+    buf = (ctypes.c_float * 64)()
+    assert L.crane_hip_rope_tables(D, 1e6, 0.0, 1, 2, buf, buf) == _lib.E_DTYPE
+    assert L.crane_hip_rope_tables(127, 1e6, 0.0, 1, 0, buf, buf) == _lib.E_INVALID
+    assert L.crane_hip_rope_tables(D, -1.0, 0.0, 1, 0, buf, buf) == _lib.E_INVALID
+    assert L.crane_hip_rope_tables(D, 1e6, -2.0, 1, 0, buf, buf) == _lib.E_INVALID
+    assert L.crane_hip_rope_tables(D, 1e6, 0.0, 1, 0, None, buf) == _lib.E_INVALID
+    assert L.crane_hip_rope_tables(D, 1e6, 0.0, 0, 0, None, None) == _lib.OK
+    assert L.crane_hip_rope_tables_qwen2(D, 0.0, 1, 1, buf, buf) == _lib.E_INVALID
 
 
 # ----------------------------------------------------------------- rmsnorm

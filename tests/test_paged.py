@@ -25,12 +25,13 @@ D = 128
 def test_paged_launcher_argument_checks():
     from crane_amd import _lib
     L = _lib.lib()
-    # (q, k, v, n_pages, page_rows, table, stride, kv_len, max_kv, B, Hq, Hkv, D, scale, ws, ws_bytes, out, dt, st)
-    base = [16, 16, 16, 64, 256, 16, 8, 16, 1024, 1, 32, 8, 128, 0.088, 16, 1 << 30, 16, 1, None]
+    # (q, k, v, n_pages, page_rows, table, stride, kv_len, max_kv, B, Hq, Hkv, D, scale, score_mode, ws, ws_bytes,
+    #  out, dt, st)
+    base = [16, 16, 16, 64, 256, 16, 8, 16, 1024, 1, 32, 8, 128, 0.088, 0, 16, 1 << 30, 16, 1, None]
 
     def dec(**kw):
         a = list(base)
-        idx = dict(n_pages=3, page_rows=4, table=5, stride=6, max_kv=8, D=12, dt=17)
+        idx = dict(n_pages=3, page_rows=4, table=5, stride=6, max_kv=8, D=12, score=14, dt=18)
         for k, v in kw.items():
             a[idx[k]] = v
         return L.crane_hip_attn_decode_paged(*a)
@@ -43,6 +44,7 @@ def test_paged_launcher_argument_checks():
     assert dec(max_kv=8 * 256 + 1) == _lib.E_CAPACITY    # more rows than the table can map
     assert dec(D=64) == _lib.E_HEAD_DIM
     assert dec(dt=5) == _lib.E_DTYPE
+    assert dec(score=2) == _lib.E_INVALID
     assert L.crane_hip_attn_prefill_paged(16, 16, 16, 64, 256, 16, 2, 16, 400, 1, 200, 32, 8, 128, 0.088, 1, 16,
                                           1, None) == _lib.E_CAPACITY  # 400 + 200 > 2 pages of 256
     assert L.crane_hip_qknorm_rope_append_paged(16, 40 * 128, None, None, 1e-6, 0, 16, 16, 64, 4096, 16, 16, 16, 16,

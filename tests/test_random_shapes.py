@@ -62,13 +62,14 @@ def test_random_decode(gpu, orc, i):
         lens[int(r.integers(0, B))] = 0  # an empty sequence
     if lens.max() == 0:
         lens[0] = 1
-    print(f"random decode {i}: B={B} Hq={Hq} Hkv={Hkv} lens={lens.tolist()} {dtype}", flush=True)
+    mode = "standard" if i % 3 == 2 else None  # every third draw takes Qwen2.5's form
+    print(f"random decode {i}: B={B} Hq={Hq} Hkv={Hkv} lens={lens.tolist()} {dtype} mode={mode}", flush=True)
     q, k, v, lens = cases.decode_case(SEED + 7200 + i, B, Hq, Hkv, lens, dtype=dtype)
     out = ops.attention_decode(_t(q, dtype, gpu), _t(k, dtype, gpu), _t(v, dtype, gpu),
-                               torch.as_tensor(lens, device=gpu), int(lens.max()), cases.scale())
+                               torch.as_tensor(lens, device=gpu), int(lens.max()), cases.scale(), score_mode=mode)
     torch.cuda.synchronize()
     got = out.float().cpu().numpy().reshape(B, Hq * D)
-    ref = orc.attn_decode(q, k, v, lens, cases.scale(), dtype)
+    ref = orc.attn_decode(q, k, v, lens, cases.scale(), dtype, cases.decode_variant(orc, Hq, Hkv, mode))
     for b in range(B):
         if lens[b] == 0:
             assert np.all(got[b] == 0), "an empty sequence's row is zero"
@@ -79,6 +80,19 @@ def test_random_decode(gpu, orc, i):
 
 @pytest.mark.parametrize("i", range(N_PREFILL))
 def test_random_prefill(gpu, orc, i):
+    _prefill_draw(gpu, orc, SEED, i)
+
+
+# Draws of the seed-offset-10000 sweep on which a kernel without candle's
+# second score rounding and its bf16 softmax of few-key rows missed the 2e-2
+# bar by one bf16 ulp at |x| >= 2 (rows with 2-8 keys, and one row of the
+# key-split variant).  Kept as fixed cases.
+@pytest.mark.parametrize("i", [7, 28, 70, 102])
+def test_prefill_rounding_tail_draws(gpu, orc, i):
+    _prefill_draw(gpu, orc, 10000, i)
+
+
+def _prefill_draw(gpu, orc, SEED, i):
     import torch
     from crane_amd import ops
     r = cases.rng(SEED + 7300 + i)
