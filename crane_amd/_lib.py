@@ -40,6 +40,9 @@ SIGNATURES = {
     "crane_hip_attn_decode_workspace": ([_i, _i, _i, _i, _i64, _i], _sz),
     "crane_hip_attn_decode": (
         [_vp, _vp, _vp, _i64, _i32p, _i64, _i, _i, _i, _i, _f, _i, _vp, _sz, _vp, _i, _vp], _i),
+    "crane_hip_attn_decode_noalloc": (
+        [_vp, _vp, _vp, _i64, _i32p, _i64, _i, _i, _i, _i, _f, _i, _vp, _i, _vp], _i),
+    "crane_hip_attn_decode_noalloc_limit": ([], _sz),
     "crane_hip_attn_prefill": (
         [_vp, _vp, _vp, _i64, _i32p, _i64, _i, _i, _i, _i, _i, _f, _i, _vp, _i, _vp], _i),
     # include/crane_kv.h

@@ -47,6 +47,7 @@
 // to T, p = T(e / sum), then p @ V with f32 accumulation): the whole row is in
 // the workgroup, so the exact chain costs nothing measurable.  Longer
 // sequences keep the split-KV form (unnormalised bf16 p per chunk, f32 sums).
+#include <mutex>
 #include <type_traits>
 
 #include "common.h"
@@ -670,6 +671,57 @@ extern "C" int crane_hip_attn_decode(const void* q, const void* k_cache, const v
     if (cache_cap <= 0 || max_kv > cache_cap) return CRANE_HIP_E_CAPACITY;
     return attn_decode(q, k_cache, v_cache, DenseRows{cache_cap}, kv_len, max_kv, B, Hq, Hkv, D, scale, score_mode,
                        workspace, ws_bytes, out, dtype, stream);
+}
+
+// ---- Allocation-free decode: the split-KV partials in a device array that
+// lives as long as the process (one copy per GPU), for callers that cannot
+// allocate (HIP graph capture, serving loops that forbid hipMalloc).  Calls
+// that overlap in time on one GPU share the array and race; the partials need
+// no clearing (each chunk's slot is written before the merge reads it).
+static constexpr size_t kScratchBytes = (size_t)32 << 20;  // 32 MiB: c5 (8 x 64 heads, 32769 keys, bf16) needs 17.0 MiB
+static __device__ __align__(256) uint8_t scratch[kScratchBytes];
+
+namespace crane {
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex scratch_mu;
+void* scratch_ptr[kMaxDevices];  // the array's device address on each GPU, looked up once per device
+
+// The array's address on the current device (set-up on the device's first
+// call: hipGetSymbolAddress with that device current).  Returns a CRANE_HIP_E_*
+// code; *ptr is valid only on success.
+int device_scratch(void** ptr) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return CRANE_HIP_E_LAUNCH;
+    std::lock_guard<std::mutex> lock(scratch_mu);
+    if (!scratch_ptr[dev]) {
+        void* p = nullptr;
+        if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) return CRANE_HIP_E_LAUNCH;
+        scratch_ptr[dev] = p;
+    }
+    *ptr = scratch_ptr[dev];
+    return CRANE_HIP_OK;
+}
+}  // namespace
+}  // namespace crane
+
+extern "C" size_t crane_hip_attn_decode_noalloc_limit(void) { return kScratchBytes; }
+
+extern "C" int crane_hip_attn_decode_noalloc(const void* q, const void* k_cache, const void* v_cache,
+                                             int64_t cache_cap, const int32_t* kv_len, int64_t max_kv, int B, int Hq,
+                                             int Hkv, int D, float scale, int score_mode, void* out, int dtype,
+                                             void* stream) {
+    if (cache_cap <= 0 || max_kv > cache_cap) return CRANE_HIP_E_CAPACITY;
+    if (dtype != CRANE_HIP_F32 && dtype != CRANE_HIP_BF16) return CRANE_HIP_E_DTYPE;
+    if (D != kHeadDim) return CRANE_HIP_E_HEAD_DIM;
+    if (B < 0 || Hq <= 0 || Hkv <= 0 || max_kv <= 0 || max_kv > 0x7fffffffLL || B > 65535) return CRANE_HIP_E_INVALID;
+    if (B == 0) return CRANE_HIP_OK;
+    if (ws_layout(B, Hq, n_splits(max_kv), dtype).total > kScratchBytes) return CRANE_HIP_E_WORKSPACE;
+    void* ws = nullptr;
+    const int rc = device_scratch(&ws);
+    if (rc) return rc;
+    return attn_decode(q, k_cache, v_cache, DenseRows{cache_cap}, kv_len, max_kv, B, Hq, Hkv, D, scale, score_mode, ws,
+                       kScratchBytes, out, dtype, stream);
 }
 
 extern "C" int crane_hip_attn_decode_paged(const void* q, const void* k_pool, const void* v_pool, int64_t n_pages,

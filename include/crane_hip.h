@@ -172,6 +172,23 @@ int crane_hip_attn_decode(const void* q, const void* k_cache, const void* v_cach
                           int Hq, int Hkv, int D, float scale, int score_mode, void* workspace,
                           size_t ws_bytes, void* out, int dtype, void* stream);
 
+/* crane_hip_attn_decode without a workspace argument, for callers that cannot
+ * allocate device memory (code under HIP graph capture, serving loops, harnesses
+ * that forbid hipMalloc).  No counterpart in the reference: Crane's candle ops
+ * allocate their outputs and temporaries per call.
+ * The split-KV partials go in a device array of the library, one per GPU, of
+ * crane_hip_attn_decode_noalloc_limit() bytes (32 MiB), held until the process
+ * ends; sizes whose crane_hip_attn_decode_workspace(...) exceeds it return
+ * CRANE_HIP_E_WORKSPACE.  The call allocates nothing (the array's address is
+ * looked up on a device's first call).  Calls that overlap in time on one GPU
+ * share the array and race: order them on one stream.  Other arguments and
+ * results as crane_hip_attn_decode. */
+int crane_hip_attn_decode_noalloc(const void* q, const void* k_cache, const void* v_cache,
+                                  int64_t cache_cap, const int32_t* kv_len, int64_t max_kv, int B,
+                                  int Hq, int Hkv, int D, float scale, int score_mode, void* out,
+                                  int dtype, void* stream);
+size_t crane_hip_attn_decode_noalloc_limit(void);
+
 /* Causal (or full) GQA prefill attention over the cache.
  *
  * q        [B, Hq, S, D] (the prefill q_out of the append)
