@@ -459,17 +459,6 @@ __global__ __launch_bounds__(64 * kWaves * SPLIT) __attribute__((amdgpu_waves_pe
                     for (int r = 0; r < 16; ++r) tmax = fmaxf(tmax, sc[nb][r]);
                 return tmax;
             };
-#ifdef PF_MAX_CHECK
-            const float tmax = tile_max();
-            if (__any(tmax * scale_log2 > m_run + 8.0f)) rescale(tmax);
-            l_run += tile_p(m_run == -INFINITY ? 0.f : -m_run);
-        }
-        // Unconditional, so this stays in one basic block with the exp work
-        // above: past the last tile (or above this wave's diagonal) the
-        // result is simply not used, and nothing is in flight into that buffer.
-        qk_tile(kbuf[par ^ 1], qf, koff, sn);
-        pv_tile(vbuf[par], pf);
-#else
             float psum = tile_p(m_run == -INFINITY ? 0.f : -m_run);
             // Unconditional, so this stays in one basic block with the exp
             // work above: past the last tile (or above this wave's diagonal)
@@ -483,7 +472,6 @@ __global__ __launch_bounds__(64 * kWaves * SPLIT) __attribute__((amdgpu_waves_pe
             l_run += psum;
         }
         pv_tile(vbuf[par], pf);
-#endif
     };
     const int n_steps = SPLIT > 1 ? half : n_tiles;
     for (int t = 0; t < n_steps; t += 2) {
