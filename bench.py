@@ -460,6 +460,67 @@ def bench_append(args, dev, stream, lib):
     return res
 
 
+# ------------------------------------------------------- whole decode step
+
+def bench_model_step(args, dev, stream, lib):
+    """One decode step of a whole Qwen3-8B-shape model at config 3's batch: 36
+    layers (hidden 4096, 32 q / 8 kv heads, intermediate 12288, QK-norm), the
+    final norm and the lm_head (vocab 151936), B=32 sequences at the config 3
+    lengths (each attends its L_i+1 rows in every layer).  The step is the
+    model driver's decode step (crane_amd/model.py) captured once in a HIP
+    graph and replayed; the lengths are put back before every replay so each
+    step is the same workload.  Random weights of the model's shapes; the
+    roofline is HBM: every weight and every layer's K/V rows are read once a
+    step."""
+    import torch
+    from crane_amd import decoder, model
+    L, H, Hq, Hkv, I, V = 36, 4096, 32, 8, 12288, 151936
+    lens = c3_lengths()
+    B = len(lens)
+    cap = int(lens.max()) + 8
+    gen = torch.Generator(device=dev).manual_seed(SEED0 + 36)
+    bf = torch.bfloat16
+
+    def w(*shape, std):
+        return randn(shape, gen, bf, dev, std)
+
+    layers = [decoder.LayerWeights(input_norm=torch.ones(H, dtype=bf, device=dev),
+                                   qkv=w((Hq + 2 * Hkv) * D, H, std=H ** -0.5), o=w(H, Hq * D, std=(Hq * D) ** -0.5),
+                                   post_norm=torch.ones(H, dtype=bf, device=dev), gate_up=w(2 * I, H, std=H ** -0.5),
+                                   down=w(H, I, std=I ** -0.5), q_norm=torch.ones(D, dtype=bf, device=dev),
+                                   k_norm=torch.ones(D, dtype=bf, device=dev)) for _ in range(L)]
+    cfg = model.ModelConfig(hidden=H, num_heads=Hq, num_kv_heads=Hkv, intermediate=I, num_layers=L, family="qwen3")
+    m = model.DecoderModel(cfg, layers, torch.ones(H, dtype=bf, device=dev), w(V, H, std=H ** -0.5), B, cap)
+    for i in range(L):
+        m.k[i].copy_(randn(m.k[i].shape, gen, bf, dev))
+        m.v[i].copy_(randn(m.v[i].shape, gen, bf, dev))
+    base = torch.as_tensor(lens, device=dev)
+    m.lengths.copy_(base)
+    m.host_lengths[:] = lens
+    g = model.DecodeGraph(m)
+    g.x.copy_(randn((B, 1, H), gen, bf, dev))
+    g.positions.copy_(base)
+
+    def launch(i):
+        m.lengths.copy_(base)
+        m.host_lengths[:] = lens
+        g.replay()
+
+    steps = max(3, args.steps // 2)
+    ms = timed(launch, steps, args.warmup, stream)
+    weight_bytes = sum(t.numel() * 2 for lw in layers for t in (lw.input_norm, lw.qkv, lw.o, lw.post_norm,
+                                                                 lw.gate_up, lw.down, lw.q_norm, lw.k_norm))
+    weight_bytes += (V * H + H) * 2
+    kv_bytes = L * int((lens + 1).sum()) * Hkv * D * 2 * 2
+    gbs = (weight_bytes + kv_bytes) / (ms * 1e-3) / 1e9
+    log(f"[model step] Qwen3-8B shape, {L} layers, B={B}: {ms:.3f} ms/step, {B / (ms * 1e-3):.0f} tokens/s, "
+        f"{gbs:.0f} GB/s of weights + K/V ({gbs / HBM_PEAK_GBS * 100:.1f}% of HBM)")
+    res = dict(ms=ms, tokens_per_s=B / (ms * 1e-3), gbs=gbs, weight_bytes=weight_bytes, kv_bytes=kv_bytes, layers=L)
+    del g, m, layers
+    torch.cuda.empty_cache()
+    return res
+
+
 # ----------------------------------------------------------- CPU baseline
 
 def _timed_runs(fn, min_seconds: float, min_runs: int):
@@ -548,7 +609,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--only", choices=["decode", "prefill", "append", "layer", "gemm", "sampling", "all"], default="all")
+    ap.add_argument("--only", choices=["decode", "prefill", "append", "layer", "gemm", "sampling", "model", "all"],
+                    default="all")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run a plain elementwise kernel over 1 GiB (scales FETCH_SIZE/WRITE_SIZE counters)")
@@ -595,6 +657,7 @@ def main():
     lay = bench_layer(args, dev, stream, lib) if args.only in ("layer", "all") else None
     gem = bench_gemm(args, dev, stream, lib) if args.only in ("gemm", "all") else None
     smp = bench_sampling(args, dev, stream, lib) if args.only in ("sampling", "all") else None
+    mod = bench_model_step(args, dev, stream, lib) if args.only in ("model", "all") else None
     cpu = {} if args.no_cpu_baseline else cpu_baseline(dec, pre)
 
     traffic = pmc_traffic()
@@ -658,6 +721,15 @@ def main():
         line["gemm"] = {t: {k: round(v, 4) for k, v in d.items()} for t, d in gem.items()}
     if smp is not None:
         line["sampling"] = {t: {k: round(v, 2) for k, v in d.items()} for t, d in smp.items()}
+    if mod is not None:
+        line["model_decode_step"] = {
+            "workload": "Qwen3-8B-shape model decode step (36 layers, final norm, lm_head 151936) at c3: B=32, "
+                        "L_i~U{512..4096}; HIP-graph replay of crane_amd.model.DecodeGraph",
+            "ms_per_step": round(mod["ms"], 4), "tokens_per_s": round(mod["tokens_per_s"], 1),
+            "roofline": {"bound": "hbm", "achieved": round(mod["gbs"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": round(mod["gbs"] / HBM_PEAK_GBS, 4),
+                         "bytes_per_step": mod["weight_bytes"] + mod["kv_bytes"],
+                         "weight_bytes": mod["weight_bytes"], "kv_bytes": mod["kv_bytes"]}}
     if "decode" in cpu:
         line["cpu_baseline"] = cpu["decode"]
     print(json.dumps(line), flush=True)

@@ -11,7 +11,9 @@
 // loaded once into registers (16-byte chunks, up to CRANE_LAYER_MAX_COLS
 // elements), the sum of squares is a DPP wave reduction, and the normalised
 // row is written from the registers, so every tensor crosses HBM exactly once
-// (add + norm: residual and hidden read, residual and out written).  Rounding
+// (add + norm: residual and hidden read, residual and out written).  With few
+// rows (a decode step) one wave per row leaves most of the chip idle and the
+// call is latency-bound; there a workgroup of 4 waves takes each row.  Rounding
 // follows candle's ops: the sum r + h is rounded to T before it is stored and
 // squared; m = sqrt(sum/cols + eps) is rounded to T; then x / m and the
 // product with the weight are each rounded to T.  SiLU * up is the f32
@@ -130,6 +132,77 @@ __global__ __launch_bounds__(64 * kRowsPerBlock) void rms_norm_kernel(T* __restr
     }
 }
 
+// Few rows (a decode step's B rows): one workgroup of 256 threads per row, so
+// the row's chunks are spread over 4 waves instead of one.  Thread t holds
+// chunks t, t + 256, ...; the weight chunks are loaded with the row (one round
+// trip to memory); the sum of squares is reduced per wave (DPP) and across the
+// 4 waves through LDS in a fixed order.  Same rounding points as
+// rms_norm_kernel.
+constexpr int kRowThreads = 256;
+
+template <typename T, bool ADD, int CH>
+__global__ __launch_bounds__(kRowThreads) void rms_norm_row_kernel(T* __restrict__ x, const T* __restrict__ hidden,
+                                                                   const T* __restrict__ w, T* __restrict__ out,
+                                                                   int cols, float eps) {
+    constexpr int N = Vec<T>::N;
+    __shared__ float part[kRowThreads / 64];
+    const int64_t row = blockIdx.x;
+    const int nch = cols / N;
+    T* xr = x + row * cols;
+    uint4 c[CH], wc[CH];
+    float ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < CH; ++i) {
+        const int idx = i * kRowThreads + (int)threadIdx.x;
+        if (idx < nch) {
+            uint4 a = ld16<ADD>(xr + idx * N);
+            if (w) wc[i] = ld16<false>(w + idx * N);
+            if constexpr (ADD) {  // residual = T(residual + hidden), stored, and normed as rounded
+                float va[N], vh[N];
+                Vec<T>::unpack(a, va);
+                Vec<T>::unpack(ld16<true>(hidden + row * cols + idx * N), vh);
+#pragma unroll
+                for (int e = 0; e < N; ++e) va[e] += vh[e];
+                a = Vec<T>::pack(va);
+                st16<true>(xr + idx * N, a);
+            }
+            c[i] = a;
+            float v[N];
+            Vec<T>::unpack(a, v);
+#pragma unroll
+            for (int e = 0; e < N; ++e) ss = __builtin_fmaf(v[e], v[e], ss);
+        }
+    }
+    ss = wave_sum(ss);
+    if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = ss;
+    __syncthreads();
+    float total = part[0];
+#pragma unroll
+    for (int v = 1; v < kRowThreads / 64; ++v) total += part[v];
+    const float m = rt<T>(sqrtf(total / (float)cols + eps));
+    T* orow = out + row * cols;
+#pragma unroll
+    for (int i = 0; i < CH; ++i) {
+        const int idx = i * kRowThreads + (int)threadIdx.x;
+        if (idx < nch) {
+            float v[N], wv[N];
+            Vec<T>::unpack(c[i], v);
+            if (w) {
+                Vec<T>::unpack(wc[i], wv);
+            } else {
+#pragma unroll
+                for (int e = 0; e < N; ++e) wv[e] = 1.f;
+            }
+#pragma unroll
+            for (int e = 0; e < N; ++e) v[e] = rt<T>(v[e] / m) * wv[e];
+            st16<true>(orow + idx * N, Vec<T>::pack(v));
+        }
+    }
+}
+
+// Row counts below this take rms_norm_row_kernel (a workgroup per row).
+constexpr int64_t kFewRows = 1024;
+
 __device__ __forceinline__ float silu(float g) { return g / (1.0f + expf(-g)); }
 
 template <typename T>
@@ -175,6 +248,21 @@ unsigned stride_grid(int64_t n_chunks) {
 
 template <typename T, bool ADD>
 int launch_norm(T* x, const T* hidden, const T* w, T* out, int64_t rows, int cols, float eps, hipStream_t st) {
+    if (rows < kFewRows) {
+        const int per_thread = (cols / Vec<T>::N + kRowThreads - 1) / kRowThreads;
+#define CRANE_ROW_CASE(ch)                                                                                       \
+        if (per_thread <= ch) {                                                                                  \
+            hipLaunchKernelGGL((rms_norm_row_kernel<T, ADD, ch>), dim3((unsigned)rows), dim3(kRowThreads), 0, st, \
+                               x, hidden, w, out, cols, eps);                                                    \
+            return launch_status(hipGetLastError());                                                             \
+        }
+        CRANE_ROW_CASE(1)
+        CRANE_ROW_CASE(2)
+        CRANE_ROW_CASE(4)
+        CRANE_ROW_CASE(8)
+#undef CRANE_ROW_CASE
+        return CRANE_HIP_E_INVALID;
+    }
     const int per_lane = (cols / Vec<T>::N + 63) / 64;
     const dim3 grid((unsigned)((rows + kRowsPerBlock - 1) / kRowsPerBlock)), block(64 * kRowsPerBlock);
 #define CRANE_NORM_CASE(ch)                                                                                   \

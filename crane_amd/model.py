@@ -113,16 +113,16 @@ class DecoderModel:
 
     # ------------------------------------------------------------------ steps
 
-    def _layer(self, i: int, x: torch.Tensor, positions: torch.Tensor, lengths_after: torch.Tensor,
-               S: int, bound: int, start_bound: int) -> torch.Tensor:
+    def _layer(self, i: int, residual: torch.Tensor, h: torch.Tensor, positions: torch.Tensor,
+               lengths_after: torch.Tensor, S: int, bound: int, start_bound: int) -> torch.Tensor:
         """DecoderLayer::forward (qwen3/modeling.rs:655-673) over the layer's
-        cache; x [B, S, hidden] is updated in place (the residual stream)."""
+        cache from its normed input h [B S, hidden]; the attention half is added
+        into `residual` in place, and the MLP output is returned for the caller
+        to add (fused with the next norm)."""
         cfg, w = self.cfg, self.layers[i]
-        B, H = self.batch, cfg.hidden
+        B = self.batch
         D, Hq, Hkv = ops.HEAD_DIM, cfg.num_heads, cfg.num_kv_heads
         eps = cfg.rms_norm_eps
-        residual = x.view(B * S, H)
-        h = ops.rms_norm(residual, w.input_norm, eps)
         a = self.anchor(i)
         if self.shared(i):
             q = ops.linear(h, w.qkv, w.qkv_bias).view(B, S, Hq * D)
@@ -137,9 +137,8 @@ class DecoderModel:
         else:
             attn = ops.attention_prefill(q, self.k[a], self.v[a], self.lengths, start_bound, self.scale, True)
         o = ops.linear(attn.view(B * S, Hq * D), w.o)
-        h = ops.add_rms_norm(residual, o, w.post_norm, eps)
-        ops.residual_add(residual, ops.linear(ops.silu_mul(ops.linear(h, w.gate_up)), w.down))
-        return x
+        h2 = ops.add_rms_norm(residual, o, w.post_norm, eps)
+        return ops.linear(ops.silu_mul(ops.linear(h2, w.gate_up)), w.down)
 
     def _run(self, x: torch.Tensor, positions: torch.Tensor, bound: int, start_bound: int) -> torch.Tensor:
         B, S, H = x.shape
@@ -147,12 +146,23 @@ class DecoderModel:
             raise CraneHipError(E_INVALID, f"x {tuple(x.shape)} {x.dtype} does not match the model")
         if positions.dtype != torch.int32 or positions.numel() != B:
             raise CraneHipError(E_INVALID, "positions must be int32 [B]")
+        eps, L = self.cfg.rms_norm_eps, self.cfg.num_layers
         x = x.contiguous().clone()       # the residual stream; the caller's tensor is not modified
+        residual = x.view(B * S, H)
         lengths_after = self.lengths + S
-        for i in range(self.cfg.num_layers):
-            self._layer(i, x, positions, lengths_after, S, bound, start_bound)
+        # each layer's last residual add is fused with the next layer's input
+        # norm (candle's residual add then RmsNorm, as one add + norm kernel)
+        h = ops.rms_norm(residual, self.layers[0].input_norm, eps)
+        for i in range(L):
+            mlp = self._layer(i, residual, h, positions, lengths_after, S, bound, start_bound)
+            if i + 1 < L:
+                h = ops.add_rms_norm(residual, mlp, self.layers[i + 1].input_norm, eps)
         self.lengths.add_(S)             # every layer appended S rows per sequence
-        last = ops.rms_norm(x[:, S - 1:, :].contiguous(), self.final_norm, self.cfg.rms_norm_eps)
+        if S == 1:                       # every row is a last position: add + final norm at once
+            last = ops.add_rms_norm(residual, mlp, self.final_norm, eps).view(B, 1, H)
+        else:
+            ops.residual_add(residual, mlp)
+            last = ops.rms_norm(x[:, S - 1:, :].contiguous(), self.final_norm, eps)
         return ops.linear(last, self.lm_head) if self.lm_head is not None else last
 
     def forward(self, x: torch.Tensor, positions: torch.Tensor) -> torch.Tensor:

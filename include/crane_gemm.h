@@ -1,7 +1,7 @@
 /*
- * crane_gemm.h -- C ABI of the projections around the attention block: the
- * merged QKV projection that feeds crane_hip_qknorm_rope_append and o_proj
- * that consumes the attention output (gfx950, hipBLASLt).
+ * crane_gemm.h -- C ABI of the projections of a decoder layer: the merged QKV
+ * projection that feeds crane_hip_qknorm_rope_append, o_proj that consumes
+ * the attention output, the MLP projections and the lm_head (gfx950).
  *
  * Crane's projections are candle Linear layers (qwen3/modeling.rs:207-223,
  * 382-387 qkv_proj; :466 and :502 o_proj; the QKV bias of Qwen2.5,
@@ -10,9 +10,13 @@
  * output [M, (Hq + 2 Hkv) D] is exactly the `qkv` rows of the fused append,
  * and the attention output [B, S, Hq D] is exactly o_proj's x.
  *
- * These are plain library GEMMs: hipBLASLt with f32 accumulation, the bias
- * added in the epilogue (one rounding of acc + b, where candle rounds the
- * product and then the sum).  A crane_gemm context holds the hipBLASLt handle,
+ * The same call serves the MLP projections (gate_up, down) and the lm_head.
+ * Products go to hipBLASLt with f32 accumulation, the bias added in the
+ * epilogue (one rounding of acc + b, where candle rounds the product and then
+ * the sum), except wide bf16 products with few token rows (M <= 32, N >= 16384:
+ * the decode step's gate_up and lm_head), which a hand-written streaming
+ * kernel runs with the same accumulation and rounding.  A crane_gemm context
+ * holds the hipBLASLt handle,
  * a workspace allocated at creation and the algorithm chosen for each shape
  * (the heuristic query runs once per shape).  Conventions otherwise as in
  * crane_hip.h; crane_gemm_linear does not allocate or synchronise.  Calls on

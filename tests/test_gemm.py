@@ -1,7 +1,8 @@
-"""The projections around the attention block (include/crane_gemm.h): candle
-Linear y = x W^T + b on hipBLASLt -- Crane's merged qkv_proj, whose rows feed
-the fused append (qwen3/modeling.rs:382-387; with the Qwen2.5 bias,
-qwen25/qwen2.rs:136-138), and o_proj (:466, :502).
+"""The projections of a decoder layer (include/crane_gemm.h): candle Linear
+y = x W^T + b -- Crane's merged qkv_proj, whose rows feed the fused append
+(qwen3/modeling.rs:382-387; with the Qwen2.5 bias, qwen25/qwen2.rs:136-138),
+o_proj (:466, :502), the MLP projections and the lm_head; on hipBLASLt, or on
+the streaming kernel for wide decode-shaped bf16 products.
 
 The oracle's linear is pinned to numpy float64 matmul (a transposed weight
 fails); the GPU is held to the oracle within the rounding bound of its two
@@ -97,6 +98,27 @@ def test_linear_parity(gpu, orc, dtype, M, N, K, bias):
     assert_linear_close(got.float().cpu().numpy(), x, w, b, dtype, orc, f"linear {M}x{N}x{K}")
     # twice: the cached plan gives the same bits
     got2 = ops.linear(_t(x, dtype, gpu), _t(w, dtype, gpu), _t(b, dtype, gpu) if bias else None)
+    assert bool((got == got2).all())
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("M,N,K,bias", [
+    (32, 16384, 1024, False),  # the decode batch of config 3; 8 stages of 128
+    (17, 16448, 384, True),    # a partial second token group; 3 stages; 257 workgroups
+    (8, 16384, 640, True),     # 5 stages: the unrolled-by-three loop's remainder of 2
+    (1, 16384, 256, True),     # one token row; 2 stages
+    (3, 20480, 128, False),    # one stage
+])
+def test_linear_streaming_parity(gpu, orc, M, N, K, bias):
+    """Wide bf16 products with few token rows run the streaming kernel
+    (M <= 32, N >= 16384, K a multiple of 128), the gate_up and lm_head shapes
+    of a decode step; same bar as the library path."""
+    from crane_amd import ops
+    print(f"linear (streaming) M={M} N={N} K={K} bias={bias}", flush=True)
+    x, w, b = _case(900 + M + K, M, N, K, "bf16", bias)
+    got = ops.linear(_t(x, "bf16", gpu), _t(w, "bf16", gpu), _t(b, "bf16", gpu) if bias else None)
+    assert_linear_close(got.float().cpu().numpy(), x, w, b, "bf16", orc, f"streaming linear {M}x{N}x{K}")
+    got2 = ops.linear(_t(x, "bf16", gpu), _t(w, "bf16", gpu), _t(b, "bf16", gpu) if bias else None)
     assert bool((got == got2).all())
 
 

@@ -12,10 +12,11 @@ import numpy as np
 import pytest
 
 import cases
-from tolerance import assert_close, assert_ulp_close, bf16_ulp
+from tolerance import BF16_MEAN_REL, assert_close, assert_ulp_close, bf16_ulp, errors
 
 # (rows, cols): Qwen3-8B decode batch, Qwen2.5-7B, Qwen2.5-72B, Qwen3-0.6B, tiny rows
-NORM_SHAPES = [(32, 4096), (257, 3584), (4, 8192), (3, 1024), (5, 8)]
+# (rows, cols): fewer than 1024 rows take a workgroup per row, more a wave per row
+NORM_SHAPES = [(32, 4096), (257, 3584), (4, 8192), (1031, 2048), (3, 1024), (5, 8)]
 # (rows, intermediate): Qwen3-8B, Qwen2.5-7B, tiny
 MLP_SHAPES = [(32, 12288), (9, 18944), (3, 8)]
 
@@ -119,6 +120,19 @@ def _np(t):
     return t.float().cpu().numpy()
 
 
+def _norm_bar(got, ref, dtype, what):
+    """The norms' bar besides assert_ulp_close (one bf16 ulp at max(|ref|, 8)
+    per element, 99.9% bit-identical): f32 max-abs, bf16 mean-relative.  The
+    bf16 max-abs 2e-2 does not apply: a normed row reaches |v| >= 4, where one
+    ulp is 2^-5 > 2e-2, and the f32 sum of squares (summed in another order
+    than the oracle's) can move a row's norm, hence all of its values, by an
+    ulp."""
+    if dtype == "f32":
+        assert_close(got, ref, dtype, what)
+    else:
+        assert errors(got, ref)[1] <= BF16_MEAN_REL, what
+
+
 @pytest.mark.gpu
 @pytest.mark.parametrize("dtype", ["bf16", "f32"])
 @pytest.mark.parametrize("rows,cols", NORM_SHAPES)
@@ -130,14 +144,14 @@ def test_rms_norm_parity(gpu, orc, dtype, rows, cols):
     got = _np(ops.rms_norm(_t(x, dtype, gpu), _t(w, dtype, gpu)))
     ref = orc.rms_norm(x, w, 1e-6, True, dtype)
     assert_ulp_close(got, ref, dtype, f"rms_norm {rows}x{cols}", min_exact=0.999)
-    assert_close(got, ref, dtype, f"rms_norm {rows}x{cols}")
+    _norm_bar(got, ref, dtype, f"rms_norm {rows}x{cols}")
     got1 = _np(ops.rms_norm(_t(x, dtype, gpu)))                          # no weight = weight 1
     assert_ulp_close(got1, orc.rms_norm(x, None, 1e-6, True, dtype), dtype, "rms_norm w=1", min_exact=0.999)
 
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("dtype", ["bf16", "f32"])
-@pytest.mark.parametrize("rows,cols", NORM_SHAPES[:3])
+@pytest.mark.parametrize("rows,cols", NORM_SHAPES[:4])
 def test_add_rms_norm_parity(gpu, orc, dtype, rows, cols):
     """The residual is updated bit-exactly (rounded sum), the norm is of that
     rounded sum."""
@@ -151,7 +165,7 @@ def test_add_rms_norm_parity(gpu, orc, dtype, rows, cols):
     new_r, ref = orc.add_rms_norm(r, h, w, 1e-6, dtype)
     np.testing.assert_array_equal(_np(rt), new_r)
     assert_ulp_close(got, ref, dtype, f"add_rms_norm {rows}x{cols}", min_exact=0.999)
-    assert_close(got, ref, dtype, f"add_rms_norm {rows}x{cols}")
+    _norm_bar(got, ref, dtype, f"add_rms_norm {rows}x{cols}")
 
 
 @pytest.mark.gpu
