@@ -338,7 +338,9 @@ def bench_gemm(args, dev, stream, lib):
 
 def bench_sampling(args, dev, stream, lib):
     """Token selection over Qwen vocabulary logits (151936): argmax on bf16
-    (greedy) and top-64 on f32, one row and a c3 batch of 32 rows."""
+    (greedy) and top-64 on f32, one row and a c3 batch of 32 rows; the
+    split-row (_ws) entry points, which the ops wrappers call, and the
+    single-pass kernels (one workgroup per row) beside them."""
     import torch
     res = {}
     st = stream.cuda_stream
@@ -348,8 +350,16 @@ def bench_sampling(args, dev, stream, lib):
         xb = randn((rows, n), gen, torch.bfloat16, dev, 4.0)
         xf = randn((rows, n), gen, torch.float32, dev, 4.0)
         out = torch.empty((rows, 64), dtype=torch.int32, device=dev)
-        for name, fn in (("argmax_bf16", lambda i: lib.crane_hip_argmax(xb.data_ptr(), rows, n, 1, out.data_ptr(), st)),
-                         ("topk64_f32", lambda i: lib.crane_hip_topk(xf.data_ptr(), rows, n, 64, out.data_ptr(), st))):
+        wsb = int(lib.crane_hip_select_workspace_bytes(rows, n))
+        ws = torch.empty(max(wsb, 16), dtype=torch.uint8, device=dev)
+        for name, fn in (("argmax_bf16", lambda i: lib.crane_hip_argmax_ws(xb.data_ptr(), rows, n, 1, ws.data_ptr(),
+                                                                            wsb, out.data_ptr(), st)),
+                         ("topk64_f32", lambda i: lib.crane_hip_topk_ws(xf.data_ptr(), rows, n, 64, ws.data_ptr(),
+                                                                         wsb, out.data_ptr(), st)),
+                         ("argmax_bf16_single_pass",
+                          lambda i: lib.crane_hip_argmax(xb.data_ptr(), rows, n, 1, out.data_ptr(), st)),
+                         ("topk64_f32_single_pass",
+                          lambda i: lib.crane_hip_topk(xf.data_ptr(), rows, n, 64, out.data_ptr(), st))):
             def launch(i, fn=fn, name=name):
                 rc = fn(i)
                 if rc:
@@ -357,6 +367,27 @@ def bench_sampling(args, dev, stream, lib):
             ms = timed(launch, args.steps, args.warmup, stream)
             res[f"{name}_rows{rows}"] = dict(us=ms * 1e3)
             log(f"[sampling] {name} {rows} x {n}: {ms * 1e3:.1f} us")
+            if not name.endswith("single_pass"):
+                # as a serving step runs it: captured with the step's other
+                # kernels in a HIP graph, so back-to-back launches cost no
+                # host round trip (graph of 10 selections, time per selection)
+                cs = torch.cuda.Stream(device=dev)
+                cs.wait_stream(stream)
+                g = torch.cuda.CUDAGraph()
+                st_c = cs.cuda_stream
+                fn_c = {"argmax_bf16": lambda: lib.crane_hip_argmax_ws(xb.data_ptr(), rows, n, 1, ws.data_ptr(), wsb,
+                                                                       out.data_ptr(), st_c),
+                        "topk64_f32": lambda: lib.crane_hip_topk_ws(xf.data_ptr(), rows, n, 64, ws.data_ptr(), wsb,
+                                                                    out.data_ptr(), st_c)}[name]
+                with torch.cuda.graph(g, stream=cs):
+                    for _ in range(10):
+                        if fn_c():
+                            raise RuntimeError(f"{name} failed under capture")
+                stream.wait_stream(cs)
+                torch.cuda.synchronize(dev)
+                msg = timed(lambda i: g.replay(), max(3, args.steps // 10), args.warmup, stream) / 10
+                res[f"{name}_rows{rows}"]["us_graph"] = msg * 1e3
+                log(f"[sampling] {name} {rows} x {n}, graph replay: {msg * 1e3:.1f} us")
     return res
 
 

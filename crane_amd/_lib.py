@@ -76,6 +76,9 @@ SIGNATURES = {
     # include/crane_sampling.h
     "crane_hip_argmax": ([_vp, _i64, _i64, _i, _vp, _vp], _i),
     "crane_hip_topk": ([_vp, _i64, _i64, _i, _vp, _vp], _i),
+    "crane_hip_select_workspace_bytes": ([_i64, _i64], _sz),
+    "crane_hip_argmax_ws": ([_vp, _i64, _i64, _i, _vp, _sz, _vp, _vp], _i),
+    "crane_hip_topk_ws": ([_vp, _i64, _i64, _i, _vp, _sz, _vp, _vp], _i),
     # include/crane_gemm.h
     "crane_gemm_create": ([_sz, _vpp], _i),
     "crane_gemm_destroy": ([_vp], None),

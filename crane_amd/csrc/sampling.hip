@@ -1,9 +1,11 @@
 // sampling.hip -- argmax and top-k over logits rows (gfx950); C ABI in
 // include/crane_sampling.h.
 //
-// Both kernels give one 1024-thread workgroup a row (a vocabulary of ~152k
-// logits is 0.3-0.6 MB, one L2's worth) and order elements by a 32-bit key that
-// is monotone in the float value (NaN mapped to 0, below -inf).
+// The single-pass kernels give one 1024-thread workgroup a row (a vocabulary
+// of ~152k logits is 0.3-0.6 MB, one L2's worth); with few rows the _ws entry
+// points split each row over many workgroups (see "split rows" below).  All
+// order elements by a 32-bit key that is monotone in the float value (NaN
+// mapped to 0, below -inf).
 //   argmax: each thread keeps the largest (key << 32 | ~index) of its
 //     16-byte chunks, so a 64-bit max is the largest value with the lowest
 //     index; wave and workgroup max with shuffles and LDS.
@@ -128,9 +130,34 @@ __device__ __forceinline__ void crossing_bin(const uint32_t* tot, uint32_t krem,
 
 constexpr int kCand = 2048;  // candidates sorted in LDS on the fast path
 
-__global__ __launch_bounds__(kThreads) void topk_kernel(const float* __restrict__ x, int64_t n, int k,
-                                                        uint32_t* __restrict__ out) {
-    const float* xr = x + (int64_t)blockIdx.x * n;
+// Sort `count` <= kCand candidates (key << 32 | ~index) held in LDS, key
+// descending then index ascending (bitonic over the next power of two, padded
+// with the lowest key), and write the first k indices; the whole workgroup
+// calls it.
+__device__ void sort_candidates(uint64_t* cand, uint32_t count, int k, uint32_t* __restrict__ out_row) {
+    const int tid = threadIdx.x;
+    uint32_t P = 64;
+    while (P < count) P <<= 1;
+    for (uint32_t i = count + tid; i < P; i += kThreads) cand[i] = 0;
+    __syncthreads();
+    for (uint32_t size = 2; size <= P; size <<= 1)
+        for (uint32_t stride = size >> 1; stride > 0; stride >>= 1) {
+            for (uint32_t p = tid; p < P / 2; p += kThreads) {
+                const uint32_t a = 2 * stride * (p / stride) + (p % stride), b = a + stride;
+                const bool desc = (a & size) == 0;
+                const uint64_t va = cand[a], vb = cand[b];
+                if ((va < vb) == desc) {
+                    cand[a] = vb;
+                    cand[b] = va;
+                }
+            }
+            __syncthreads();
+        }
+    if (tid < k) out_row[tid] = ~(uint32_t)cand[tid];
+}
+
+// The exact top-k of one row by one workgroup of kThreads threads.
+__device__ void topk_block(const float* __restrict__ xr, int64_t n, int k, uint32_t* __restrict__ out_row) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     __shared__ uint32_t hist[kWavesT][256];
     __shared__ uint32_t tot[256];
@@ -218,27 +245,8 @@ __global__ __launch_bounds__(kThreads) void topk_kernel(const float* __restrict_
     });
     __syncthreads();
     const uint32_t count = s_count;
-    if (count <= kCand) {
-        // Fast path: sort the candidates, key descending then index ascending
-        // (bitonic over the next power of two, padded with the lowest key).
-        uint32_t P = 64;
-        while (P < count) P <<= 1;
-        for (uint32_t i = count + tid; i < P; i += kThreads) cand[i] = 0;
-        __syncthreads();
-        for (uint32_t size = 2; size <= P; size <<= 1)
-            for (uint32_t stride = size >> 1; stride > 0; stride >>= 1) {
-                for (uint32_t p = tid; p < P / 2; p += kThreads) {
-                    const uint32_t a = 2 * stride * (p / stride) + (p % stride), b = a + stride;
-                    const bool desc = (a & size) == 0;
-                    const uint64_t va = cand[a], vb = cand[b];
-                    if ((va < vb) == desc) {
-                        cand[a] = vb;
-                        cand[b] = va;
-                    }
-                }
-                __syncthreads();
-            }
-        if (tid < k) out[(int64_t)blockIdx.x * k + tid] = ~(uint32_t)cand[tid];
+    if (count <= kCand) {  // fast path: sort the candidates
+        sort_candidates(cand, count, k, out_row);
         return;
     }
 
@@ -286,8 +294,238 @@ __global__ __launch_bounds__(kThreads) void topk_kernel(const float* __restrict_
                 const bool desc = (lane & size) == 0, low = (lane & stride) == 0;
                 v = (low == desc) ? (o > v ? o : v) : (o < v ? o : v);
             }
-        if (lane < k) out[(int64_t)blockIdx.x * k + lane] = ~(uint32_t)v;
+        if (lane < k) out_row[lane] = ~(uint32_t)v;
     }
+}
+
+__global__ __launch_bounds__(kThreads) void topk_kernel(const float* __restrict__ x, int64_t n, int k,
+                                                        uint32_t* __restrict__ out) {
+    topk_block(x + (int64_t)blockIdx.x * n, n, k, out + (int64_t)blockIdx.x * k);
+}
+
+// ------------------------------------------------------------------ split rows
+//
+// Few rows: one workgroup per row would leave most of the chip idle (a
+// 152k-entry row is 0.3-0.6 MB), so each row is cut into P slices of L
+// elements (P >= 64 workgroups per row) and the work goes in phases, each a
+// kernel, that meet in the caller's workspace (a kernel boundary is the only
+// synchronisation: nothing to clear, no counters, no fences):
+//   argmax:  (1) each slice's largest (key << 32 | ~index);  (2) the largest of
+//            the P of a row.
+//   top-k:   (1) each slice's largest key, and slice 0 zeroes the row's
+//            candidate count;  (2) every workgroup of a row computes t, the
+//            k-th largest of the P slice maxima -- k elements of distinct
+//            slices are >= t, so t is a lower bound of the row's k-th largest
+//            and every answer has a key >= t -- and appends its slice's keys
+//            >= t to the row's candidate list (wave-aggregated atomics);
+//            (3) one workgroup per row ranks the candidates (a few hundred for
+//            real logits; a thread's rank is the count of larger candidates)
+//            or sorts them (more than 1024) and writes the first k, or, when
+//            more than kCand reached t (long runs of equal values), runs the
+//            exact one-workgroup path over the row.
+// (Merging the phases into one kernel, the last workgroup of a row to arrive
+// doing the merge, needs an agent-scope release / acquire per workgroup; at
+// these sizes those fences cost more than the launches they save.)
+constexpr int kSplitThreads = 256;
+constexpr int kSplitMinParts = CRANE_TOPK_MAX;  // P >= k, so the slice-max bound holds
+constexpr int kSplitMaxParts = 256;
+constexpr int64_t kSplitMinN = 32768;
+constexpr int64_t kSplitMaxRows = 32;
+
+// Slice [p L, min(n, p L + L)) of row xr as (key, index) pairs.
+template <typename T, typename F>
+__device__ __forceinline__ void for_slice(const T* __restrict__ xr, int64_t n, int64_t L, int p, F&& f) {
+    constexpr int N = 16 / sizeof(T);
+    const int64_t i0 = (int64_t)p * L, i1 = min(n, i0 + L);
+    const bool vec = (i0 % N) == 0 && (((uintptr_t)(xr + i0)) & 15) == 0;
+    int64_t i = i0;
+    if (vec) {
+        const int64_t nv = (i1 - i0) / N;
+        for (int64_t c = threadIdx.x; c < nv; c += kSplitThreads) {
+            const uint4 u = *reinterpret_cast<const uint4*>(xr + i0 + c * N);
+            const uint32_t* w = reinterpret_cast<const uint32_t*>(&u);
+#pragma unroll
+            for (int e = 0; e < N; ++e) {
+                float v;
+                if constexpr (sizeof(T) == 4) v = __uint_as_float(w[e]);
+                else v = (e & 1) ? bf16_hi(w[e >> 1]) : bf16_lo(w[e >> 1]);
+                f(fkey(v), (uint32_t)(i0 + c * N + e));
+            }
+        }
+        i = i0 + nv * N;
+    }
+    for (int64_t j = i + threadIdx.x; j < i1; j += kSplitThreads) f(fkey(elem(xr + j)), (uint32_t)j);
+}
+
+// Largest of v over the workgroup (kSplitThreads threads); every thread gets it.
+__device__ __forceinline__ uint64_t block_max64(uint64_t v) {
+    __shared__ uint64_t wmax[kSplitThreads / 64];
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) {
+        const uint64_t o = shfl_xor64(v, m);
+        v = o > v ? o : v;
+    }
+    if ((threadIdx.x & 63) == 0) wmax[threadIdx.x >> 6] = v;
+    __syncthreads();
+    uint64_t r = wmax[0];
+#pragma unroll
+    for (int w = 1; w < kSplitThreads / 64; ++w) r = wmax[w] > r ? wmax[w] : r;
+    return r;
+}
+
+template <typename T>
+__global__ __launch_bounds__(kSplitThreads) void argmax_part_kernel(const T* __restrict__ x, int64_t n, int64_t L,
+                                                                    uint64_t* __restrict__ part) {
+    const int p = blockIdx.x, row = blockIdx.y;
+    uint64_t best = 0;
+    for_slice<T>(x + (int64_t)row * n, n, L, p, [&](uint32_t key, uint32_t i) {
+        const uint64_t kk = ((uint64_t)key << 32) | (uint32_t)~i;
+        best = kk > best ? kk : best;
+    });
+    best = block_max64(best);
+    if (threadIdx.x == 0) part[(int64_t)row * gridDim.x + p] = best;
+}
+
+__global__ __launch_bounds__(64) void argmax_final_kernel(const uint64_t* __restrict__ part, int P,
+                                                          uint32_t* __restrict__ out) {
+    const int row = blockIdx.x;
+    uint64_t best = 0;
+    for (int p = threadIdx.x; p < P; p += 64) {
+        const uint64_t v = part[(int64_t)row * P + p];
+        best = v > best ? v : best;
+    }
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) {
+        const uint64_t o = shfl_xor64(best, m);
+        best = o > best ? o : best;
+    }
+    if (threadIdx.x == 0) out[row] = ~(uint32_t)best;
+}
+
+// Per-row block of the top-k workspace: the candidate count, the P slice
+// maxima, then kCand candidates (8-byte aligned).
+__host__ __device__ __forceinline__ int64_t topk_cand_offset(int P) { return ((4 + 4 * (int64_t)P + 7) / 8) * 8; }
+__host__ __device__ __forceinline__ int64_t topk_row_bytes(int P) { return topk_cand_offset(P) + 8 * (int64_t)kCand; }
+
+__global__ __launch_bounds__(kSplitThreads) void topk_max_kernel(const float* __restrict__ x, int64_t n, int64_t L,
+                                                                 uint8_t* __restrict__ ws) {
+    const int p = blockIdx.x, P = gridDim.x, row = blockIdx.y;
+    uint32_t* hdr = reinterpret_cast<uint32_t*>(ws + (int64_t)row * topk_row_bytes(P));
+    uint64_t best = 0;
+    for_slice<float>(x + (int64_t)row * n, n, L, p, [&](uint32_t key, uint32_t) {
+        best = key > best ? key : best;
+    });
+    best = block_max64(best);
+    if (threadIdx.x == 0) {
+        hdr[1 + p] = (uint32_t)best;
+        if (p == 0) hdr[0] = 0u;  // the candidate count, for the next kernel
+    }
+}
+
+// The k-th largest of the P (<= kSplitMaxParts) keys m[0..P), by one wave:
+// the largest t with at least k keys >= t, bit by bit from the top.
+__device__ __forceinline__ uint32_t kth_largest_wave(const uint32_t* m, int P, int k, int lane) {
+    uint32_t v[kSplitMaxParts / 64];
+#pragma unroll
+    for (int j = 0; j < kSplitMaxParts / 64; ++j) v[j] = 64 * j + lane < P ? m[64 * j + lane] : 0u;
+    uint32_t t = 0;
+    for (int bit = 31; bit >= 0; --bit) {
+        const uint32_t c = t | (1u << bit);
+        int cnt = 0;
+#pragma unroll
+        for (int j = 0; j < kSplitMaxParts / 64; ++j) cnt += __popcll(__ballot(v[j] >= c));
+        if (cnt >= k) t = c;
+    }
+    return t;
+}
+
+__global__ __launch_bounds__(kSplitThreads) void topk_collect_kernel(const float* __restrict__ x, int64_t n, int64_t L,
+                                                                     int k, uint8_t* __restrict__ ws) {
+    const int p = blockIdx.x, P = gridDim.x, row = blockIdx.y;
+    const int lane = threadIdx.x & 63;
+    uint8_t* rb = ws + (int64_t)row * topk_row_bytes(P);
+    uint32_t* hdr = reinterpret_cast<uint32_t*>(rb);
+    uint64_t* cand = reinterpret_cast<uint64_t*>(rb + topk_cand_offset(P));
+    const float* xr = x + (int64_t)row * n;
+    const int64_t i0 = (int64_t)p * L, i1 = min(n, i0 + L);
+    const bool vec = (i0 % 4) == 0 && (((uintptr_t)(xr + i0)) & 15) == 0;
+    const int64_t nv = vec ? (i1 - i0) / 4 : 0;
+    // this thread's first 16 bytes of the slice, in flight while t is computed
+    const int64_t c0 = threadIdx.x;
+    const float4 first = c0 < nv ? *reinterpret_cast<const float4*>(xr + i0 + 4 * c0) : make_float4(0.f, 0.f, 0.f, 0.f);
+    __shared__ uint32_t s_t;
+    if (threadIdx.x < 64) {
+        const uint32_t tw = kth_largest_wave(hdr + 1, P, k, lane);
+        if (lane == 0) s_t = tw;
+    }
+    __syncthreads();
+    const uint32_t t = s_t;
+    auto take = [&](uint32_t key, uint32_t i) __attribute__((always_inline)) {
+        const bool tk = key >= t;
+        const uint64_t b = __ballot(tk);
+        if (b == 0) return;  // uniform per wave
+        uint32_t base = 0;
+        const int leader = __ffsll((unsigned long long)b) - 1;
+        if (lane == leader) base = atomicAdd(&hdr[0], (uint32_t)__popcll(b));
+        base = __shfl(base, leader);
+        const uint32_t slot = base + (uint32_t)__popcll(b & ((1ull << lane) - 1ull));
+        if (tk && slot < (uint32_t)kCand) cand[slot] = ((uint64_t)key << 32) | (uint32_t)~i;
+    };
+    for (int64_t c = c0; c < nv; c += kSplitThreads) {
+        const float4 v = c == c0 ? first : *reinterpret_cast<const float4*>(xr + i0 + 4 * c);
+        const uint32_t i = (uint32_t)(i0 + 4 * c);
+        take(fkey(v.x), i);
+        take(fkey(v.y), i + 1);
+        take(fkey(v.z), i + 2);
+        take(fkey(v.w), i + 3);
+    }
+    for (int64_t j = i0 + 4 * nv + threadIdx.x; j < i1; j += kSplitThreads) take(fkey(xr[j]), (uint32_t)j);
+}
+
+__global__ __launch_bounds__(kThreads) void topk_final_kernel(const float* __restrict__ x, int64_t n, int k, int P,
+                                                              const uint8_t* __restrict__ ws,
+                                                              uint32_t* __restrict__ out) {
+    const int row = blockIdx.x;
+    const uint8_t* rb = ws + (int64_t)row * topk_row_bytes(P);
+    const uint32_t count = *reinterpret_cast<const uint32_t*>(rb);
+    uint32_t* out_row = out + (int64_t)row * k;
+    if (count > (uint32_t)kCand) {  // uniform: long runs of equal values
+        topk_block(x + (int64_t)row * n, n, k, out_row);
+        return;
+    }
+    __shared__ uint64_t cand[kCand];
+    const uint64_t* src = reinterpret_cast<const uint64_t*>(rb + topk_cand_offset(P));
+    for (uint32_t i = threadIdx.x; i < count; i += kThreads) cand[i] = src[i];
+    __syncthreads();
+    if (count <= (uint32_t)kThreads) {
+        // Up to one candidate per thread: its rank is the number of larger
+        // candidates (the keys are distinct: the index is part of them), read
+        // back from LDS as broadcasts; ranks below k are the answer, in order.
+        const uint64_t mine = threadIdx.x < count ? cand[threadIdx.x] : 0;
+        uint32_t rank = 0;
+        for (uint32_t j = 0; j < count; ++j) rank += cand[j] > mine ? 1u : 0u;
+        if (threadIdx.x < count && rank < (uint32_t)k) out_row[rank] = ~(uint32_t)mine;
+    } else {
+        sort_candidates(cand, count, k, out_row);
+    }
+}
+
+// Slices of a row for the split path: P workgroups of L elements (L a whole
+// number of 16-byte chunks), P = 0 when the row is taken whole.
+struct Split {
+    int P;
+    int64_t L;
+};
+
+Split split_of(int64_t rows, int64_t n) {
+    if (rows > kSplitMaxRows || n < kSplitMinN) return {0, 0};
+    int64_t P = n / 1024;
+    P = P < kSplitMinParts ? kSplitMinParts : (P > kSplitMaxParts ? kSplitMaxParts : P);
+    int64_t L = (n + P - 1) / P;
+    L = (L + 7) / 8 * 8;
+    const int64_t used = (n + L - 1) / L;  // non-empty slices
+    if (used < kSplitMinParts) return {0, 0};
+    return {(int)used, L};
 }
 
 }  // namespace
@@ -317,5 +555,56 @@ extern "C" int crane_hip_topk(const float* x, int64_t rows, int64_t n, int k, ui
     if (rows == 0) return CRANE_HIP_OK;
     if (!x || !out_idx) return CRANE_HIP_E_INVALID;
     hipLaunchKernelGGL(topk_kernel, dim3((unsigned)rows), dim3(kThreads), 0, (hipStream_t)stream, x, n, k, out_idx);
+    return launch_status(hipGetLastError());
+}
+
+extern "C" size_t crane_hip_select_workspace_bytes(int64_t rows, int64_t n) {
+    if (rows <= 0 || n <= 0) return 0;
+    const Split sp = split_of(rows, n);
+    if (sp.P == 0) return 0;
+    const int64_t arg = rows * sp.P * 8, top = rows * topk_row_bytes(sp.P);
+    return (size_t)(arg > top ? arg : top);
+}
+
+extern "C" int crane_hip_argmax_ws(const void* logits, int64_t rows, int64_t n, int dtype, void* workspace,
+                                   size_t ws_bytes, uint32_t* out_idx, void* stream) {
+    if (dtype != CRANE_HIP_F32 && dtype != CRANE_HIP_BF16) return CRANE_HIP_E_DTYPE;
+    if (rows < 0 || n <= 0 || n > 0x7fffffffLL || rows > 0x7fffffffLL) return CRANE_HIP_E_INVALID;
+    if (rows == 0) return CRANE_HIP_OK;
+    const Split sp = split_of(rows, n);
+    if (sp.P == 0) return crane_hip_argmax(logits, rows, n, dtype, out_idx, stream);
+    if (!logits || !out_idx) return CRANE_HIP_E_INVALID;
+    if (!workspace || ws_bytes < crane_hip_select_workspace_bytes(rows, n) || ((uintptr_t)workspace & 15))
+        return CRANE_HIP_E_CAPACITY;
+    hipStream_t st = (hipStream_t)stream;
+    uint64_t* part = (uint64_t*)workspace;
+    const dim3 grid((unsigned)sp.P, (unsigned)rows);
+    if (dtype == CRANE_HIP_F32)
+        hipLaunchKernelGGL(argmax_part_kernel<float>, grid, dim3(kSplitThreads), 0, st, (const float*)logits, n, sp.L,
+                           part);
+    else
+        hipLaunchKernelGGL(argmax_part_kernel<bf16_t>, grid, dim3(kSplitThreads), 0, st, (const bf16_t*)logits, n,
+                           sp.L, part);
+    hipLaunchKernelGGL(argmax_final_kernel, dim3((unsigned)rows), dim3(64), 0, st, part, sp.P, out_idx);
+    return launch_status(hipGetLastError());
+}
+
+extern "C" int crane_hip_topk_ws(const float* x, int64_t rows, int64_t n, int k, void* workspace, size_t ws_bytes,
+                                 uint32_t* out_idx, void* stream) {
+    if (rows < 0 || n <= 0 || n > 0x7fffffffLL || rows > 0x7fffffffLL) return CRANE_HIP_E_INVALID;
+    if (k < 1 || k > CRANE_TOPK_MAX || (int64_t)k > n) return CRANE_HIP_E_INVALID;
+    if (rows == 0) return CRANE_HIP_OK;
+    const Split sp = split_of(rows, n);
+    if (sp.P == 0) return crane_hip_topk(x, rows, n, k, out_idx, stream);
+    if (!x || !out_idx) return CRANE_HIP_E_INVALID;
+    if (!workspace || ws_bytes < crane_hip_select_workspace_bytes(rows, n) || ((uintptr_t)workspace & 15))
+        return CRANE_HIP_E_CAPACITY;
+    hipStream_t st = (hipStream_t)stream;
+    uint8_t* ws = (uint8_t*)workspace;
+    const dim3 grid((unsigned)sp.P, (unsigned)rows);
+    hipLaunchKernelGGL(topk_max_kernel, grid, dim3(kSplitThreads), 0, st, x, n, sp.L, ws);
+    hipLaunchKernelGGL(topk_collect_kernel, grid, dim3(kSplitThreads), 0, st, x, n, sp.L, k, ws);
+    hipLaunchKernelGGL(topk_final_kernel, dim3((unsigned)rows), dim3(kThreads), 0, st, x, n, k, sp.P,
+                       (const uint8_t*)ws, out_idx);
     return launch_status(hipGetLastError());
 }

@@ -541,9 +541,17 @@ def argmax(logits: torch.Tensor) -> torch.Tensor:
     n = logits.shape[-1]
     rows = logits.numel() // max(n, 1)
     out = torch.empty(logits.shape[:-1], dtype=torch.int32, device=dev)
-    check(_lib.lib().crane_hip_argmax(logits.data_ptr(), rows, n, _dtype_code(logits), out.data_ptr(), _stream(dev)),
-          "argmax")
+    ws, wsb = _select_workspace(rows, n, dev)
+    check(_lib.lib().crane_hip_argmax_ws(logits.data_ptr(), rows, n, _dtype_code(logits), _ptr(ws), wsb,
+                                         out.data_ptr(), _stream(dev)), "argmax")
     return out
+
+
+def _select_workspace(rows: int, n: int, dev: torch.device):
+    """The split-row workspace of argmax / top-k (None when the shape takes the
+    single-pass kernels); it holds nothing between calls."""
+    wsb = int(_lib.lib().crane_hip_select_workspace_bytes(rows, n))
+    return (torch.empty(wsb, dtype=torch.uint8, device=dev) if wsb else None), wsb
 
 
 def topk_indices(x: torch.Tensor, k: int) -> torch.Tensor:
@@ -556,5 +564,7 @@ def topk_indices(x: torch.Tensor, k: int) -> torch.Tensor:
     n = x.shape[-1]
     rows = x.numel() // max(n, 1)
     out = torch.empty(x.shape[:-1] + (k,), dtype=torch.int32, device=dev)
-    check(_lib.lib().crane_hip_topk(x.data_ptr(), rows, n, k, out.data_ptr(), _stream(dev)), "topk_indices")
+    ws, wsb = _select_workspace(rows, n, dev)
+    check(_lib.lib().crane_hip_topk_ws(x.data_ptr(), rows, n, k, _ptr(ws), wsb, out.data_ptr(), _stream(dev)),
+          "topk_indices")
     return out

@@ -55,6 +55,25 @@ def test_sampling_argument_checks():
     assert L.crane_hip_topk(None, 1, 100, 8, 16, None) == _lib.E_INVALID
 
 
+def test_split_workspace_and_checks():
+    """The split path applies to few (<= 32) long (>= 32768) rows; elsewhere
+    the workspace size is 0 and the _ws calls run the single-pass kernels."""
+    from crane_amd import _lib
+    L = _lib.lib()
+    assert L.crane_hip_select_workspace_bytes(1, VOCAB) > 0
+    assert L.crane_hip_select_workspace_bytes(32, VOCAB) >= 32 * L.crane_hip_select_workspace_bytes(1, VOCAB) // 2
+    assert L.crane_hip_select_workspace_bytes(33, VOCAB) == 0
+    assert L.crane_hip_select_workspace_bytes(1, 32767) == 0
+    assert L.crane_hip_select_workspace_bytes(0, VOCAB) == 0
+    need = L.crane_hip_select_workspace_bytes(2, VOCAB)
+    assert L.crane_hip_argmax_ws(16, 2, VOCAB, 1, None, 0, 16, None) == _lib.E_CAPACITY
+    assert L.crane_hip_argmax_ws(16, 2, VOCAB, 1, 16, need - 1, 16, None) == _lib.E_CAPACITY
+    assert L.crane_hip_topk_ws(16, 2, VOCAB, 64, None, 0, 16, None) == _lib.E_CAPACITY
+    assert L.crane_hip_topk_ws(16, 2, VOCAB, 65, 16, need, 16, None) == _lib.E_INVALID
+    assert L.crane_hip_argmax_ws(16, 2, VOCAB, 3, 16, need, 16, None) == _lib.E_DTYPE
+    assert L.crane_hip_argmax_ws(16, 0, VOCAB, 1, None, 0, 16, None) == _lib.OK
+
+
 # ------------------------------------------------------------------ GPU
 
 def _t(x, dtype, dev):
@@ -122,3 +141,98 @@ def test_topk_ties_straddling_k(gpu, orc):
     for k in (64, 33, 1):
         got = ops.topk_indices(_t(x, "f32", gpu), k).cpu().numpy().astype(np.uint32)
         np.testing.assert_array_equal(got, orc.topk(x, k), err_msg=f"k={k}")
+
+
+@pytest.mark.gpu
+def test_split_rows_ties_masks_and_nan(gpu, orc):
+    """The split path (few rows of the vocabulary's length, 148 workgroups a
+    row) on the tie, mask and NaN rows: equal maxima in different slices, a
+    row of equal values (more candidates than the list holds: the exact
+    one-workgroup fallback), fewer finite values than k, NaN runs."""
+    from crane_amd import _lib, ops
+    n = VOCAB
+    assert _lib.lib().crane_hip_select_workspace_bytes(8, n) > 0
+    x = cases.bf16(_logits(50, 8, n, std=1.0))
+    x[0, [17, 40000, 151935]] = 9.0               # equal maxima in three slices
+    x[1, :] = 2.0                                 # all equal
+    x[2, :] = -np.inf
+    x[2, [7, 151935, 300]] = 1.0                  # fewer finite values than k
+    x[3, 100000:100100] = 50.0                    # 100 equal maxima inside two slices
+    x[4, ::3] = np.nan
+    x[5, 10:30] = 7.0
+    x[5, 5] = 8.0
+    x[6, :] = np.nan
+    x[7, 1000:3000] = 30.0                        # 2000 equal maxima: k of them by index
+    print("split rows: argmax", flush=True)
+    for dtype in ("bf16", "f32"):
+        got = ops.argmax(_t(x, dtype, gpu)).cpu().numpy().astype(np.uint32)
+        np.testing.assert_array_equal(got, orc.argmax(x), err_msg=dtype)
+    for k in (64, 33, 1):
+        print(f"split rows: topk k={k}", flush=True)
+        got = ops.topk_indices(_t(x, "f32", gpu), k).cpu().numpy().astype(np.uint32)
+        np.testing.assert_array_equal(got, orc.topk(x, k), err_msg=f"k={k}")
+
+
+@pytest.mark.gpu
+def test_split_workspace_shared_across_calls(gpu):
+    """One workspace (filled with garbage first) serves argmax and top-k calls
+    of different row counts in any order: it holds nothing between calls."""
+    import torch
+    from crane_amd import _lib
+    L = _lib.lib()
+    st = torch.cuda.current_stream(gpu).cuda_stream
+    wsb = L.crane_hip_select_workspace_bytes(32, VOCAB)
+    ws = torch.full((wsb,), 0x5A, dtype=torch.uint8, device=gpu)
+    x = _t(_logits(70, 32, VOCAB), "f32", gpu)
+    for rows, k in ((1, 64), (32, 50), (7, 1), (32, 64), (2, 17), (1, 3)):
+        print(f"shared workspace: rows {rows} k {k}", flush=True)
+        a = torch.empty((rows, k), dtype=torch.int32, device=gpu)
+        b = torch.empty((rows, k), dtype=torch.int32, device=gpu)
+        assert L.crane_hip_topk_ws(x.data_ptr(), rows, VOCAB, k, ws.data_ptr(), wsb, a.data_ptr(), st) == 0
+        assert L.crane_hip_topk(x.data_ptr(), rows, VOCAB, k, b.data_ptr(), st) == 0
+        c = torch.empty(rows, dtype=torch.int32, device=gpu)
+        d = torch.empty(rows, dtype=torch.int32, device=gpu)
+        assert L.crane_hip_argmax_ws(x.data_ptr(), rows, VOCAB, 0, ws.data_ptr(), wsb, c.data_ptr(), st) == 0
+        assert L.crane_hip_argmax(x.data_ptr(), rows, VOCAB, 0, d.data_ptr(), st) == 0
+        assert torch.equal(a, b) and torch.equal(c, d), (rows, k)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("rows,n", [(1, VOCAB), (32, VOCAB), (3, 32768), (2, 50001), (5, 152064)])
+def test_split_matches_single_pass(gpu, rows, n):
+    """The _ws (split) and single-pass entry points give the same indices, bit
+    for bit, at the edges of the split's range (odd n, unaligned rows, 64
+    slices)."""
+    import torch
+    from crane_amd import _lib
+    L = _lib.lib()
+    print(f"split vs single pass {rows}x{n}", flush=True)
+    x = _t(_logits(60 + rows + n, rows, n), "f32", gpu)
+    xb = x.to(torch.bfloat16)
+    wsb = L.crane_hip_select_workspace_bytes(rows, n)
+    assert wsb > 0
+    ws = torch.full((wsb,), 0xA5, dtype=torch.uint8, device=gpu)   # no initial value is needed
+    st = torch.cuda.current_stream(gpu).cuda_stream
+    for dt, t in ((0, x), (1, xb)):
+        a = torch.empty(rows, dtype=torch.int32, device=gpu)
+        b = torch.empty(rows, dtype=torch.int32, device=gpu)
+        assert L.crane_hip_argmax(t.data_ptr(), rows, n, dt, a.data_ptr(), st) == 0
+        assert L.crane_hip_argmax_ws(t.data_ptr(), rows, n, dt, ws.data_ptr(), wsb, b.data_ptr(), st) == 0
+        assert torch.equal(a, b), f"argmax dtype {dt}"
+    for k in (64, 5):
+        a = torch.empty((rows, k), dtype=torch.int32, device=gpu)
+        b = torch.empty((rows, k), dtype=torch.int32, device=gpu)
+        assert L.crane_hip_topk(x.data_ptr(), rows, n, k, a.data_ptr(), st) == 0
+        assert L.crane_hip_topk_ws(x.data_ptr(), rows, n, k, ws.data_ptr(), wsb, b.data_ptr(), st) == 0
+        assert torch.equal(a, b), f"topk k={k}"
+    # repeated calls on the same workspace keep giving the single-pass answer
+    for _ in range(3):
+        c = torch.empty(rows, dtype=torch.int32, device=gpu)
+        assert L.crane_hip_argmax_ws(xb.data_ptr(), rows, n, 1, ws.data_ptr(), wsb, c.data_ptr(), st) == 0
+        d = torch.empty((rows, 64), dtype=torch.int32, device=gpu)
+        assert L.crane_hip_topk_ws(x.data_ptr(), rows, n, 64, ws.data_ptr(), wsb, d.data_ptr(), st) == 0
+        e = torch.empty((rows, 64), dtype=torch.int32, device=gpu)
+        assert L.crane_hip_topk(x.data_ptr(), rows, n, 64, e.data_ptr(), st) == 0
+        f = torch.empty(rows, dtype=torch.int32, device=gpu)
+        assert L.crane_hip_argmax(xb.data_ptr(), rows, n, 1, f.data_ptr(), st) == 0
+        assert torch.equal(c, f) and torch.equal(d, e)
