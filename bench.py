@@ -709,6 +709,10 @@ def main():
                          "kernel": "decode_chunk_kernel + decode_merge_kernel (one crane_hip_attn_decode call)",
                          "algo_bytes_per_launch": dec["algo_bytes"]},
             "ms_p10_p50_p90": dec["pct"],
+            "statistic": "value and ms_per_step: mean over the K timed back-to-back launches (one event pair "
+                         "around all K, caches rotated over 3 copies); ms_p10_p50_p90: 100 individually "
+                         "event-timed launches after the timed region; value_p50: GB/s at that median",
+            "value_p50": round(dec["algo_bytes"] / (dec["pct"][1] * 1e-3) / 1e9, 2),
         })
     if pre is not None:
         pre_obj = {"metric": "prefill attn TFLOP/s (c4: Qwen2.5-7B shape, B=8, S=4096, 28/4 heads, causal, bf16)",

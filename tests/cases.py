@@ -99,3 +99,27 @@ def prefill_truth(q, k, v, start, b, r0, r1, causal=True):
         p = np.exp(s - s.max(1, keepdims=True))
         out[:, h] = (p / p.sum(1, keepdims=True)) @ V
     return out
+
+
+def _draw_heads(r):
+    n_rep = int(r.choice([1, 2, 3, 4, 5, 6, 7, 8, 16]))
+    hkv = int(r.choice([1, 2, 4]))
+    return n_rep * hkv, hkv
+
+
+def prefill_draw(seed: int, i: int):
+    """Draw i of the randomised prefill sweep at seed offset `seed`: (dtype, B,
+    S, Hq, Hkv, start, causal) and its inputs (q, k, v, start array)."""
+    r = rng(seed + 7300 + i)
+    dtype = "f32" if i % 5 == 4 else "bf16"
+    Hq, Hkv = _draw_heads(r)
+    B = int(r.integers(1, 4))
+    S = int(r.choice([1, 31, 64, 65, 127, 128, 129, 300, int(r.integers(1, 700))]))
+    if dtype == "f32":
+        S = min(S, 200)
+    start = [int(r.choice([0, 0, int(r.integers(1, 400))])) for _ in range(B)]
+    causal = bool(r.random() < 0.8)
+    while S > 1 and B * Hq * S * (max(start) + S) > 3e7:  # keep the oracle within seconds
+        S //= 2
+    q, k, v, st = prefill_case(seed + 7400 + i, B, S, Hq, Hkv, start, dtype=dtype)
+    return (dtype, B, S, Hq, Hkv, start, causal), (q, k, v, st)

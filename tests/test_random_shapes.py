@@ -92,22 +92,11 @@ def test_prefill_rounding_tail_draws(gpu, orc, i):
     _prefill_draw(gpu, orc, 10000, i)
 
 
-def _prefill_draw(gpu, orc, SEED, i):
+def _prefill_draw(gpu, orc, seed, i):
     import torch
     from crane_amd import ops
-    r = cases.rng(SEED + 7300 + i)
-    dtype = "f32" if i % 5 == 4 else "bf16"
-    Hq, Hkv = _heads(r)
-    B = int(r.integers(1, 4))
-    S = int(r.choice([1, 31, 64, 65, 127, 128, 129, 300, int(r.integers(1, 700))]))
-    if dtype == "f32":
-        S = min(S, 200)
-    start = [int(r.choice([0, 0, int(r.integers(1, 400))])) for _ in range(B)]
-    causal = bool(r.random() < 0.8)
-    while S > 1 and B * Hq * S * (max(start) + S) > 3e7:  # keep the oracle within seconds
-        S //= 2
+    (dtype, B, S, Hq, Hkv, start, causal), (q, k, v, st) = cases.prefill_draw(seed, i)
     print(f"random prefill {i}: B={B} S={S} Hq={Hq} Hkv={Hkv} start={start} causal={causal} {dtype}", flush=True)
-    q, k, v, st = cases.prefill_case(SEED + 7400 + i, B, S, Hq, Hkv, start, dtype=dtype)
     out = ops.attention_prefill(_t(q, dtype, gpu), _t(k, dtype, gpu), _t(v, dtype, gpu),
                                 torch.as_tensor(st, device=gpu), int(st.max()), cases.scale(), causal)
     torch.cuda.synchronize()
