@@ -77,12 +77,12 @@ def test_decode_parity(gpu, orc, name, B, Hq, Hkv, lens, dtype, std, mode):
 
 
 def test_decode_c5_long_context(gpu, orc):
-    """Config 5 (Qwen2.5-72B shape, 32768-token cache, K/V ~ N(0, 0.5)) on 2
-    of the 8 sequences, so the oracle stays within seconds."""
+    """Config 5 at full size (Qwen2.5-72B shape, B=8, 64 / 8 heads,
+    32768-token cache, K/V ~ N(0, 0.5)): every sequence against the oracle."""
     from crane_amd import ops
-    B, Hq, Hkv, L = 2, 64, 8, 32768
-    note("decode c5: B=2 Hq=64 Hkv=8 L=32768 bf16")
-    q, k, v, lens = cases.decode_case(cases.SEED0 + 5, B, Hq, Hkv, [L, L], dtype="bf16",
+    B, Hq, Hkv, L = 8, 64, 8, 32768
+    note("decode c5: B=8 Hq=64 Hkv=8 L=32768 bf16")
+    q, k, v, lens = cases.decode_case(cases.SEED0 + 5, B, Hq, Hkv, [L] * B, dtype="bf16",
                                       std=math.sqrt(0.5), poison=False)
     out = ops.attention_decode(dev_t(q, "bf16", gpu), dev_t(k, "bf16", gpu), dev_t(v, "bf16", gpu),
                                i32(lens, gpu), L, score_mode="standard")
