@@ -26,10 +26,9 @@
 // Rounding points (bf16): candle's bf16 matmul returns Q K^T rounded to bf16,
 // and its affine multiplies that by the scale converted to bf16 and rounds the
 // product to bf16 again (qwen3/modeling.rs:488); both roundings are
-// reproduced for every score.  The first packs two scores with one
-// v_cvt_pk_bf16_f32; the product of two bf16 values is exact in f32 and comes
-// from v_dot2_f32_bf16 against (scale, 0) or (0, scale); the second rounding
-// is a v_cvt_pk_bf16_f32 with a zero low half, read back as an f32.
+// reproduced for every score: each rounding is a v_cvt_pk_bf16_f32 with a
+// zero low half, read back as an f32, and the product of the two bf16 values
+// is exact in f32 (a v_mul_f32).
 // candle's softmax_last_dim then rounds s - max, exp, the row sum and the
 // quotient p = e / sum to bf16 before the P V product (:493-494).  A one-pass
 // kernel only has the row's max and sum at the end, so for rows with more than
@@ -134,34 +133,22 @@ __device__ __forceinline__ void qk_tile(const uint8_t* kt_lds, const bf16x8_v (&
         }
 }
 
-// candle's bf16 scores of four raw f32 products (two rounded pairs w0, w1 =
-// bf16(Q K^T)): s = bf16(bf16(acc) * scale), with scale a bf16 value held as
-// the pairs (scale, 0) and (0, scale).  Each product of two bf16 values is
-// exact in f32 and comes from v_dot2_f32_bf16 with a zero accumulator; the
-// rounding is v_cvt_pk_bf16_f32 with a zero low half, read as an f32.  Written
-// as instructions because the compiler clears a register for each product's
-// accumulator and rounds into the low half before moving it up (a v_mov and a
-// v_perm per score).  gfx950 lets another VALU instruction read a v_dot2
-// result only 3 instructions after it is written, so the four products are
-// formed first: each rounding reads its product exactly 3 instructions later.
-// The inputs come from ordinary VALU instructions (no MFMA result is read
-// here), and every output is an ordinary VALU result.  A masked key carries
-// the finite raw score kMaskRaw (an infinite one would turn its partner's
-// product with 0 into NaN); it stays a huge negative score.
-__device__ __forceinline__ void scores_bf16x4(uint32_t w0, uint32_t w1, uint32_t sc_lo, uint32_t sc_hi, float& s0,
-                                              float& s1, float& s2, float& s3) {
-    float x0, x1, x2, x3;
-    asm("v_dot2_f32_bf16 %4, %8, %10, 0\n\t"
-        "v_dot2_f32_bf16 %5, %8, %11, 0\n\t"
-        "v_dot2_f32_bf16 %6, %9, %10, 0\n\t"
-        "v_dot2_f32_bf16 %7, %9, %11, 0\n\t"
-        "v_cvt_pk_bf16_f32 %0, 0, %4\n\t"
-        "v_cvt_pk_bf16_f32 %1, 0, %5\n\t"
-        "v_cvt_pk_bf16_f32 %2, 0, %6\n\t"
-        "v_cvt_pk_bf16_f32 %3, 0, %7"
-        : "=&v"(s0), "=&v"(s1), "=&v"(s2), "=&v"(s3), "=&v"(x0), "=&v"(x1), "=&v"(x2), "=&v"(x3)
-        : "v"(w0), "v"(w1), "s"(sc_lo), "s"(sc_hi));
+// candle's bf16 rounding of an f32 (round to nearest even), read back as an
+// f32: v_cvt_pk_bf16_f32 with a zero low half.  Written as an instruction
+// because the compiler rounds into the low half and moves it up.  A masked
+// key carries the finite raw score kMaskRaw, which stays a huge negative
+// score through both roundings.
+__device__ __forceinline__ float round_bf16(float x) {
+    float r;
+    asm("v_cvt_pk_bf16_f32 %0, 0, %1" : "=v"(r) : "v"(x));
+    return r;
 }
+// candle's bf16 score of a raw f32 product: s = bf16(bf16(acc) * scale), with
+// scale a bf16 value held as an f32.  The product of two bf16 values is exact
+// in f32, so a plain v_mul_f32 forms it: no v_dot2_f32_bf16, which on gfx950
+// does not run beside the MFMAs (a dot2 and an MFMA stream on one SIMD take
+// longer together than one after the other).
+__device__ __forceinline__ float score_bf16(float acc, float scale) { return round_bf16(round_bf16(acc) * scale); }
 
 // Keep a value in a register as computed: the compiler may not split it into
 // a base plus a per-use offset (which would cost an add per use in the loop).
@@ -278,8 +265,8 @@ __global__ __launch_bounds__(64 * kWaves * SPLIT) __attribute__((amdgpu_waves_pe
     // Every key this wave's rows see lies in tile 0: candle's softmax chain runs exactly.
     const bool exact = grp == 0 && (CAUSAL ? wave_first + 31 < kBN : L <= kBN);
     // the bf16 scale as the pairs (scale, 0) and (0, scale), and as an f32
-    const uint32_t sc_lo = scale_bits, sc_hi = scale_bits << 16;
-    const float scale_log2 = __uint_as_float(sc_hi) * kLog2e;  // raw-score scale of the running max
+    const float scale_f = __uint_as_float(scale_bits << 16);  // the bf16 scale as an f32
+    const float scale_log2 = scale_f * kLog2e;                 // raw-score scale of the running max
     // transposed-read coordinates of this lane for the V^T fragments
     const int vg = lane >> 4, vi = lane & 15;
     const int v_h = vg >> 1;                            // key half of the A operand
@@ -347,9 +334,8 @@ __global__ __launch_bounds__(64 * kWaves * SPLIT) __attribute__((amdgpu_waves_pe
             for (int nb = 0; nb < 2; ++nb)
 #pragma unroll
                 for (int r = 0; r < 16; r += 4) {
-                    float s0, s1, s2, s3;
-                    scores_bf16x4(pack_bf16x2(sa[nb][r], sa[nb][r + 1]), pack_bf16x2(sa[nb][r + 2], sa[nb][r + 3]), sc_lo,
-                                  sc_hi, s0, s1, s2, s3);
+                    const float s0 = score_bf16(sa[nb][r], scale_f), s1 = score_bf16(sa[nb][r + 1], scale_f);
+                    const float s2 = score_bf16(sa[nb][r + 2], scale_f), s3 = score_bf16(sa[nb][r + 3], scale_f);
                     sa[nb][r] = s0;
                     sa[nb][r + 1] = s1;
                     sa[nb][r + 2] = s2;
@@ -416,8 +402,8 @@ __global__ __launch_bounds__(64 * kWaves * SPLIT) __attribute__((amdgpu_waves_pe
 #pragma unroll
                     for (int r = 0; r < 16; r += 4) {
                         float sv[4];
-                        scores_bf16x4(pack_bf16x2(sc[nb][r], sc[nb][r + 1]), pack_bf16x2(sc[nb][r + 2], sc[nb][r + 3]),
-                                      sc_lo, sc_hi, sv[0], sv[1], sv[2], sv[3]);
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) sv[e] = score_bf16(sc[nb][r + e], scale_f);
 #pragma unroll
                         for (int u = 0; u < 4; u += 2) {
                             const float p0 = fast_exp2(__builtin_fmaf(sv[u], kLog2e, neg_m));
