@@ -204,16 +204,18 @@ __global__ __launch_bounds__(kRowThreads) void rms_norm_row_kernel(T* __restrict
 constexpr int64_t kFewRows = 1024;
 
 __device__ __forceinline__ float silu(float g) { return g / (1.0f + expf(-g)); }
-
+// grid (ceil(chunks per row / 256), row slots): thread x of workgroup
+// (bx, by) owns chunk 256 bx + x of rows by, by + gridDim.y, ...  A flat
+// chunk index needed a 64-bit division per chunk, which made the kernel
+// compute-bound (config 4 rows: 773.6 -> 670.4 us, 60.2% -> 69.4% of HBM).
 template <typename T>
 __global__ __launch_bounds__(256) void silu_mul_kernel(const T* __restrict__ gu, T* __restrict__ out, int inter,
-                                                       int64_t n_chunks) {
+                                                       int64_t rows) {
     constexpr int N = Vec<T>::N;
     const int cpr = inter / N;  // chunks per output row
-    for (int64_t c = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; c < n_chunks;
-         c += (int64_t)gridDim.x * blockDim.x) {
-        const int64_t r = c / cpr;
-        const int j = (int)(c % cpr);
+    const int j = (int)blockIdx.x * 256 + (int)threadIdx.x;
+    if (j >= cpr) return;
+    for (int64_t r = blockIdx.y; r < rows; r += gridDim.y) {
         const T* g = gu + r * 2 * inter + (int64_t)j * N;
         float gv[N], uv[N];
         Vec<T>::unpack(ld16<false>(g), gv);
@@ -332,14 +334,14 @@ extern "C" int crane_hip_silu_mul(const void* gate_up, void* out, int64_t rows, 
     if (rows == 0) return CRANE_HIP_OK;
     if (!gate_up || !out) return CRANE_HIP_E_INVALID;
     if (!aligned16(gate_up) || !aligned16(out)) return CRANE_HIP_E_ALIGN;
-    const int64_t n_chunks = rows * (inter / N);
+    const dim3 grid((unsigned)((inter / N + 255) / 256), (unsigned)(rows < 16384 ? rows : 16384));
     hipStream_t st = (hipStream_t)stream;
     if (dtype == CRANE_HIP_F32)
-        hipLaunchKernelGGL(silu_mul_kernel<float>, dim3(stride_grid(n_chunks)), dim3(256), 0, st,
-                           (const float*)gate_up, (float*)out, inter, n_chunks);
+        hipLaunchKernelGGL(silu_mul_kernel<float>, grid, dim3(256), 0, st, (const float*)gate_up, (float*)out, inter,
+                           rows);
     else
-        hipLaunchKernelGGL(silu_mul_kernel<bf16_t>, dim3(stride_grid(n_chunks)), dim3(256), 0, st,
-                           (const bf16_t*)gate_up, (bf16_t*)out, inter, n_chunks);
+        hipLaunchKernelGGL(silu_mul_kernel<bf16_t>, grid, dim3(256), 0, st, (const bf16_t*)gate_up, (bf16_t*)out,
+                           inter, rows);
     return launch_status(hipGetLastError());
 }
 

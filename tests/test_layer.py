@@ -184,14 +184,17 @@ def test_silu_mul_parity(gpu, orc, dtype, rows, inter):
 
 
 @pytest.mark.gpu
-def test_silu_mul_special_values(gpu, orc):
-    import torch
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_silu_mul_special_values(gpu, orc, dtype):
+    """Zeros, large and very negative gates; in bf16 the values below -80 take
+    the kernel's exact fallback (the hardware reciprocal of 1 + e^-g would
+    flush to zero there)."""
     from crane_amd import ops
     g = np.array([0.0, -0.0, 40.0, -200.0, 1.0, -1.0, 88.0, -88.0], np.float32)
     u = np.array([3.0, 3.0, 0.5, 7.0, 2.0, 2.0, 1.0, 1.0], np.float32)
     gu = np.concatenate([g, u])[None]
-    got = _np(ops.silu_mul(torch.from_numpy(gu).to(gpu)))
-    np.testing.assert_array_equal(got, orc.silu_mul(gu, False, "f32"))
+    got = _np(ops.silu_mul(_t(gu, dtype, gpu)))
+    np.testing.assert_array_equal(got, orc.silu_mul(gu, False, dtype))
 
 
 @pytest.mark.gpu
