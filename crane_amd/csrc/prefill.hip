@@ -383,13 +383,14 @@ __global__ __launch_bounds__(64 * kWaves * SPLIT) __attribute__((amdgpu_waves_pe
         if (CAUSAL && kt > wave_first + 31) return;  // the whole tile is above this wave's diagonal
         if (exact) return;                           // done before the loop (its only tile is tile 0)
         if (kt + kBN > kend || (CAUSAL && kt + kBN - 1 > wave_first)) {  // diagonal or last tile
+            // key = kt + 4 hh + e(nb, r) is masked when key >= kend or, causal,
+            // key > qpos: one compare of the lane-constant offset e per key
+            const int thr = (CAUSAL ? min(qpos, kend - 1) : kend - 1) - kt - 4 * hh;
 #pragma unroll
             for (int nb = 0; nb < 2; ++nb)
 #pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    const int key = kt + nb * 32 + 8 * (r >> 2) + 4 * hh + (r & 3);
-                    if (key >= kend || (CAUSAL && key > qpos)) sc[nb][r] = kMaskRaw;
-                }
+                for (int r = 0; r < 16; ++r)
+                    if (nb * 32 + 8 * (r >> 2) + (r & 3) > thr) sc[nb][r] = kMaskRaw;
         }
         bf16x8_v pf[4];
         {
@@ -418,17 +419,19 @@ __global__ __launch_bounds__(64 * kWaves * SPLIT) __attribute__((amdgpu_waves_pe
             };
             // Lazy rescaling: the reference max m_run stays where it is while
             // every lane's tile sum of p stays at most kPsumMax (so every p <=
-            // kPsumMax; no max over the tile is taken).  Otherwise (including
-            // the first tile, where m_run = -inf gives p = inf) the wave moves
-            // m_run to each row's running max, rescales O and l, and takes the
-            // tile's p again.  A row that has seen no key keeps m = -inf, with
-            // p = exp2(huge negative) = 0.
-            auto rescale = [&](float tmax) __attribute__((always_inline)) {
-                // tmax: this lane half's raw max; the row's max over both halves
-                // in the log2 domain (the scale is positive); no key: -inf
+            // kPsumMax; no max over the tile is taken).  Otherwise the wave
+            // moves m_run to each row's running max, rescales O and l, and
+            // takes the tile's p again; a wave with a row at m = -inf (no key
+            // seen yet) moves first.  A row that has seen no key keeps
+            // m = -inf, with p = exp2(huge negative) = 0.
+            // tmax: this lane half's raw max; the row's max over both halves in
+            // the log2 domain (the scale is positive); no key: -inf
+            auto row_max_log2 = [&](float tmax) __attribute__((always_inline)) {
                 tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
-                tmax = tmax > 0.5f * kMaskRaw ? tmax * scale_log2 : -INFINITY;
-                const float m_new = fmaxf(m_run, tmax);
+                return tmax > 0.5f * kMaskRaw ? tmax * scale_log2 : -INFINITY;
+            };
+            auto rescale = [&](float tmax) __attribute__((always_inline)) {
+                const float m_new = fmaxf(m_run, row_max_log2(tmax));
                 const float alpha = m_new == -INFINITY ? 1.f : fast_exp2(m_run - m_new);
                 l_run *= alpha;
 #pragma unroll
@@ -445,6 +448,10 @@ __global__ __launch_bounds__(64 * kWaves * SPLIT) __attribute__((amdgpu_waves_pe
                     for (int r = 0; r < 16; ++r) tmax = fmaxf(tmax, sc[nb][r]);
                 return tmax;
             };
+            // A wave whose rows have seen no key yet (m = -inf, O = 0, l = 0,
+            // where p would be inf): m moves to the row's max first, rather
+            // than taking the tile's p twice.
+            if (__all(m_run == -INFINITY)) m_run = row_max_log2(tile_max());
             float psum = tile_p(m_run == -INFINITY ? 0.f : -m_run);
             // Unconditional, so this stays in one basic block with the exp
             // work above: past the last tile (or above this wave's diagonal)
