@@ -121,6 +121,13 @@ def lib() -> ctypes.CDLL:
             raise ImportError(
                 f"{LIB_PATH} is not built; run `python -m crane_amd.build` (hipcc, gfx950). "
                 "crane_amd has no CPU fallback.")
+        # One HIP runtime per process: torch carries its own libamdhip64 and
+        # libhipblaslt (soname libamdhip64.so.7).  Loaded first, they satisfy
+        # this library's dependencies; loaded after it, they come in beside
+        # the /opt/rocm copies its runpath names, and torch's streams and
+        # memory then belong to another runtime than its kernels (launch
+        # failures, then crashes).
+        import torch  # noqa: F401
         L = ctypes.CDLL(LIB_PATH)
         for name, (args, res) in SIGNATURES.items():
             fn = getattr(L, name)

@@ -43,6 +43,24 @@ def test_library_exports_every_declared_symbol():
         assert len(_lib.SIGNATURES[name][0]) == nargs, name
 
 
+def test_one_hip_runtime_per_process():
+    """Loading the library before torch must not leave two HIP runtimes in the
+    process (torch carries its own libamdhip64; the library's runpath names
+    the /opt/rocm one): the loader brings torch's in first.  Run in a fresh
+    interpreter, where nothing has imported torch yet."""
+    import subprocess
+    import sys
+    code = ("import sys; sys.path.insert(0, %r)\n"
+            "from crane_amd import _lib\n"
+            "_lib.lib()\n"
+            "import torch\n"
+            "maps = open('/proc/self/maps').read().split('\\n')\n"
+            "print(len({l.split()[-1] for l in maps if 'libamdhip64' in l}))\n") % ROOT
+    out = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, timeout=300)
+    assert out.returncode == 0, out.stderr
+    assert out.stdout.strip().splitlines()[-1] == "1", out.stdout
+
+
 def test_strerror_and_version():
     assert _lib.version().startswith("crane_hip 2 gfx950")
     for code in range(0, 9):
