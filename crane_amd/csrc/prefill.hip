@@ -25,10 +25,16 @@
 //
 // Rounding points (bf16): candle's bf16 matmul returns Q K^T rounded to bf16,
 // and its affine multiplies that by the scale converted to bf16 and rounds the
-// product to bf16 again (qwen3/modeling.rs:488); both roundings are
-// reproduced for every score: each rounding is a v_cvt_pk_bf16_f32 with a
-// zero low half, read back as an f32, and the product of the two bf16 values
-// is exact in f32 (a v_mul_f32).
+// product to bf16 again (qwen3/modeling.rs:488).  Workgroups whose rows see
+// fewer than kLongRowKeys keys reproduce both roundings for every score: each
+// rounding is a v_cvt_pk_bf16_f32 with a zero low half, read back as an f32,
+// and the product of the two bf16 values is exact in f32 (a v_mul_f32).
+// Workgroups whose first row sees at least kLongRowKeys keys keep the first
+// rounding only and fold the scale into the exp2 argument's FMA: two VALU
+// instructions fewer per score (the kernel is as much VALU- as MFMA-bound),
+// while over that many keys the second rounding's effect on an output
+// averages out (about 7% of the time at config 4, and 1.3e-3 more
+// mean-relative distance from candle's chain on such rows).
 // candle's softmax_last_dim then rounds s - max, exp, the row sum and the
 // quotient p = e / sum to bf16 before the P V product (:493-494).  A one-pass
 // kernel only has the row's max and sum at the end, so for rows with more than
@@ -62,6 +68,8 @@ constexpr int kBN = 64;                       // keys per tile
 constexpr int kTileBytes = kBN * kHeadDim * 2;  // 16 KiB of K (or V) per tile
 constexpr float kPsumMax = 256.0f;            // largest tile sum of p in a lane before the running max moves
 constexpr float kMaskRaw = -1.0e30f;          // raw score of a masked key (finite: see scores_bf16)
+constexpr int kLongRowKeys = 1024;           // keys a workgroup's first row sees for its rows to be long
+constexpr int kLongRowRounding = 1;          // candle's score roundings kept in long rows (of 2)
 
 __device__ __forceinline__ f32x16_v mfma32(bf16x8_v a, bf16x8_v b, f32x16_v c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
@@ -177,28 +185,18 @@ __device__ __forceinline__ bool map_block(int id, int n_qt, int B, int Hkv, int 
     return true;
 }
 
-// SPLIT = 2 (a grid too small to fill the chip): 8 waves, two groups of 4 on
-// the same 128 query rows; group g walks its half of the key tiles through its
-// own LDS tiles, and group 1's running (max, sum, O) merge into group 0's
-// through LDS at the end.  Every wave passes the same barriers: a step past a
-// group's half does no copy and no work.
-template <bool CAUSAL, class ROWS, int SPLIT>
-__global__ __launch_bounds__(64 * kWaves * SPLIT) __attribute__((amdgpu_waves_per_eu(2, 2))) void prefill_bf16_kernel(
-    const bf16_t* __restrict__ q, const bf16_t* __restrict__ kc, const bf16_t* __restrict__ vc, ROWS rows,
-    const int32_t* __restrict__ start_pos, int max_start, int S, int B, int Hq, int Hkv, uint32_t scale_bits,
-    bf16_t* __restrict__ out) {
+// The kernel body (prefill_bf16_kernel below).  R: the score roundings of candle that the workgroup's waves reproduce (2:
+// both, for rows that see fewer than kLongRowKeys keys; kLongRowRounding for
+// the rest).
+template <bool CAUSAL, class ROWS, int SPLIT, int R>
+__device__ __forceinline__ void prefill_bf16_body(const bf16_t* __restrict__ q, const bf16_t* __restrict__ kc,
+                                                  const bf16_t* __restrict__ vc, const ROWS& rows, int start, int S,
+                                                  int Hq, int Hkv, uint32_t scale_bits, bf16_t* __restrict__ out,
+                                                  int qt, int b, int hq, uint8_t (&kbufs)[SPLIT][2][kTileBytes],
+                                                  uint8_t (&vbufs)[SPLIT][2][kTileBytes]) {
     const int n_rep = Hq / Hkv;
-    const int n_qt = (S + kBM - 1) / kBM;
-    int qt, b, hq;
-    if (!map_block(blockIdx.x, n_qt, B, Hkv, n_rep, qt, b, hq)) return;
     const int kvh = hq / n_rep;
-    const int start = min(max(start_pos[b], 0), max_start);
     const int m0 = qt * kBM;
-
-    // K tiles t and t+1 and V tile t are resident while tile t is computed;
-    // K(t+2) and V(t+1) are in flight.  One set per group.
-    __shared__ __attribute__((aligned(1024))) uint8_t kbufs[SPLIT][2][kTileBytes];
-    __shared__ __attribute__((aligned(1024))) uint8_t vbufs[SPLIT][2][kTileBytes];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -408,21 +406,24 @@ __global__ __launch_bounds__(64 * kWaves * SPLIT) __attribute__((amdgpu_waves_pe
         }
         bf16x8_v pf[4];
         {
-            // p = exp2(s log2(e) - m) for candle's bf16 score s of every key,
-            // bf16 for the P V product, summed as rounded.
+            // p = exp2(s log2(e) - m) for the score s of every key, bf16 for
+            // the P V product, summed as rounded.
             auto tile_p = [&](float neg_m) __attribute__((always_inline)) {
                 float psum = 0.f;
 #pragma unroll
                 for (int nb = 0; nb < 2; ++nb)
 #pragma unroll
                     for (int r = 0; r < 16; r += 4) {
-                        float sv[4];
+                        float sv[4];  // the exp2 argument's score and its factor
 #pragma unroll
-                        for (int e = 0; e < 4; ++e) sv[e] = score_bf16(sc[nb][r + e], scale_f);
+                        for (int e = 0; e < 4; ++e)
+                            sv[e] = R == 2 ? score_bf16(sc[nb][r + e], scale_f)
+                                           : (R == 1 ? round_bf16(sc[nb][r + e]) : sc[nb][r + e]);
+                        const float fac = R == 2 ? kLog2e : scale_log2;
 #pragma unroll
                         for (int u = 0; u < 4; u += 2) {
-                            const float p0 = fast_exp2(__builtin_fmaf(sv[u], kLog2e, neg_m));
-                            const float p1 = fast_exp2(__builtin_fmaf(sv[u + 1], kLog2e, neg_m));
+                            const float p0 = fast_exp2(__builtin_fmaf(sv[u], fac, neg_m));
+                            const float p1 = fast_exp2(__builtin_fmaf(sv[u + 1], fac, neg_m));
                             const bf16x2_v pw = __builtin_bit_cast(bf16x2_v, pack_bf16x2(p0, p1));
                             psum = __builtin_amdgcn_fdot2_f32_bf16(pw, ones, psum, false);
                             pf[nb * 2 + (r >> 3)][(r & 7) + u] = pw[0];
@@ -531,6 +532,35 @@ __global__ __launch_bounds__(64 * kWaves * SPLIT) __attribute__((amdgpu_waves_pe
                 *reinterpret_cast<uint2*>(op + dim) = w;
             }
     }
+}
+
+// SPLIT = 2 (a grid too small to fill the chip): 8 waves, two groups of 4 on
+// the same 128 query rows; group g walks its half of the key tiles through its
+// own LDS tiles, and group 1's running (max, sum, O) merge into group 0's
+// through LDS at the end.  Every wave passes the same barriers: a step past a
+// group's half does no copy and no work.
+template <bool CAUSAL, class ROWS, int SPLIT>
+__global__ __launch_bounds__(64 * kWaves * SPLIT) __attribute__((amdgpu_waves_per_eu(2, 2))) void prefill_bf16_kernel(
+    const bf16_t* __restrict__ q, const bf16_t* __restrict__ kc, const bf16_t* __restrict__ vc, ROWS rows,
+    const int32_t* __restrict__ start_pos, int max_start, int S, int B, int Hq, int Hkv, uint32_t scale_bits,
+    bf16_t* __restrict__ out) {
+    const int n_rep = Hq / Hkv;
+    const int n_qt = (S + kBM - 1) / kBM;
+    int qt, b, hq;
+    if (!map_block(blockIdx.x, n_qt, B, Hkv, n_rep, qt, b, hq)) return;
+    const int start = min(max(start_pos[b], 0), max_start);
+    // K tiles t and t+1 and V tile t are resident while tile t is computed;
+    // K(t+2) and V(t+1) are in flight.  One set per group.
+    __shared__ __attribute__((aligned(1024))) uint8_t kbufs[SPLIT][2][kTileBytes];
+    __shared__ __attribute__((aligned(1024))) uint8_t vbufs[SPLIT][2][kTileBytes];
+    // The workgroup's first row sees at least kLongRowKeys keys (and so does every other row).
+    const bool long_rows = CAUSAL ? start + qt * kBM + 1 >= kLongRowKeys : start + S >= kLongRowKeys;
+    if (long_rows)
+        prefill_bf16_body<CAUSAL, ROWS, SPLIT, kLongRowRounding>(q, kc, vc, rows, start, S, Hq, Hkv, scale_bits, out,
+                                                                 qt, b, hq, kbufs, vbufs);
+    else
+        prefill_bf16_body<CAUSAL, ROWS, SPLIT, 2>(q, kc, vc, rows, start, S, Hq, Hkv, scale_bits, out, qt, b, hq,
+                                                  kbufs, vbufs);
 }
 
 // f32: one wave per (query row, q head, sequence); lane owns dims 2*lane, 2*lane+1.
