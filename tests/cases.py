@@ -123,3 +123,20 @@ def prefill_draw(seed: int, i: int):
         S //= 2
     q, k, v, st = prefill_case(seed + 7400 + i, B, S, Hq, Hkv, start, dtype=dtype)
     return (dtype, B, S, Hq, Hkv, start, causal), (q, k, v, st)
+
+
+def prefill_long_draw(seed: int, i: int):
+    """Draw i of the long-row prefill sweep: chunks that continue a cache of
+    900-3600 rows, so every row sees about 1000 keys or more (the prefill
+    kernel's long-row arithmetic), bf16."""
+    r = rng(seed + 7700 + i)
+    Hq, Hkv = _draw_heads(r)
+    B = int(r.integers(1, 3))
+    S = int(r.choice([64, 129, 300, int(r.integers(1, 400))]))
+    start = [int(r.integers(900, 3600)) for _ in range(B)]
+    causal = bool(r.random() < 0.8)
+    while S > 1 and B * Hq * S * (max(start) + S) > 3e7:  # keep the oracle within seconds
+        S //= 2
+    q, k, v, st = prefill_case(seed + 7800 + i, B, S, Hq, Hkv, start, dtype="bf16")
+    return ("bf16", B, S, Hq, Hkv, start, causal), (q, k, v, st)
+

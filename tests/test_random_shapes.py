@@ -9,8 +9,8 @@ read are NaN (the case generators poison them).
 
 The draw counts and a seed offset can be raised from the environment for a
 wider sweep (CRANE_RANDOM_DECODE, CRANE_RANDOM_PREFILL, CRANE_RANDOM_APPEND,
-CRANE_RANDOM_SEED); the defaults are the committed 24 / 20 / 12 draws at
-offset 0."""
+CRANE_RANDOM_PREFILL_LONG, CRANE_RANDOM_SEED); the defaults are the committed
+24 / 20 / 12 / 10 draws at offset 0."""
 
 import os
 
@@ -26,6 +26,7 @@ D = 128
 N_DECODE = int(os.environ.get("CRANE_RANDOM_DECODE", 24))
 N_PREFILL = int(os.environ.get("CRANE_RANDOM_PREFILL", 20))
 N_APPEND = int(os.environ.get("CRANE_RANDOM_APPEND", 12))
+N_PREFILL_LONG = int(os.environ.get("CRANE_RANDOM_PREFILL_LONG", 10))
 SEED = int(os.environ.get("CRANE_RANDOM_SEED", 0))
 
 
@@ -92,10 +93,17 @@ def test_prefill_rounding_tail_draws(gpu, orc, i):
     _prefill_draw(gpu, orc, 10000, i)
 
 
-def _prefill_draw(gpu, orc, seed, i):
+# Continuation chunks over caches of 900-3600 rows: the workgroups whose rows
+# see at least 1024 keys keep candle's first score rounding only.
+@pytest.mark.parametrize("i", range(N_PREFILL_LONG))
+def test_random_prefill_long_rows(gpu, orc, i):
+    _prefill_draw(gpu, orc, SEED, i, cases.prefill_long_draw)
+
+
+def _prefill_draw(gpu, orc, seed, i, draw=cases.prefill_draw):
     import torch
     from crane_amd import ops
-    (dtype, B, S, Hq, Hkv, start, causal), (q, k, v, st) = cases.prefill_draw(seed, i)
+    (dtype, B, S, Hq, Hkv, start, causal), (q, k, v, st) = draw(seed, i)
     print(f"random prefill {i}: B={B} S={S} Hq={Hq} Hkv={Hkv} start={start} causal={causal} {dtype}", flush=True)
     out = ops.attention_prefill(_t(q, dtype, gpu), _t(k, dtype, gpu), _t(v, dtype, gpu),
                                 torch.as_tensor(st, device=gpu), int(st.max()), cases.scale(), causal)
