@@ -199,6 +199,11 @@ size_t crane_hip_attn_decode_noalloc_limit(void);
  * causal   1: key j is visible to query i iff j <= start_pos[b]+i
  *          (qwen3/modeling.rs:866-884); 0: all start_pos[b]+S keys are visible
  * out      [B, S, Hq*D] (qwen3/modeling.rs:497-500)
+ * bf16 scores follow candle's two roundings ((q@K^T) rounded to T, then
+ * * scale rounded to T, :487-488) in query tiles whose rows see fewer than
+ * 1024 keys, and the first rounding only where every row sees 1024 keys or
+ * more; rows whose keys all lie in the first 64 get candle's softmax chain in
+ * T exactly.
  * Replaces: qwen3/modeling.rs:469-502 (see the file header). */
 int crane_hip_attn_prefill(const void* q, const void* k_cache, const void* v_cache,
                            int64_t cache_cap, const int32_t* start_pos, int64_t max_start,
