@@ -54,10 +54,22 @@ __device__ __forceinline__ void rms_norm8(float (&x1)[8], float (&x2)[8], const 
 #pragma unroll
         for (int i = 0; i < 8; ++i) w1[i] = w2[i] = 1.f;
     }
+    // x / m from one reciprocal per row (div_by) when every row of the wave has
+    // a normal, moderate m (m >= sqrt(eps) is never 0 for eps > 0); the
+    // division otherwise (an infinite or NaN input, a zero eps)
+    if (__all(m >= 0x1p-60f && m <= 0x1p60f)) {
+        const float r = 1.0f / m;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        x1[i] = rt<T>(rt<T>(x1[i] / m) * w1[i]);
-        x2[i] = rt<T>(rt<T>(x2[i] / m) * w2[i]);
+        for (int i = 0; i < 8; ++i) {
+            x1[i] = rt<T>(rt<T>(div_by(x1[i], m, r)) * w1[i]);
+            x2[i] = rt<T>(rt<T>(div_by(x2[i], m, r)) * w2[i]);
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            x1[i] = rt<T>(rt<T>(x1[i] / m) * w1[i]);
+            x2[i] = rt<T>(rt<T>(x2[i] / m) * w2[i]);
+        }
     }
 }
 

@@ -88,7 +88,30 @@ __device__ __forceinline__ void store8(bf16_t* p, const float (&v)[8]) {
 // round-to-nearest-even bf16 for bf16 (half::bf16 arithmetic rounds every op).
 template <typename T> __device__ __forceinline__ float rt(float x);
 template <> __device__ __forceinline__ float rt<float>(float x) { return x; }
-template <> __device__ __forceinline__ float rt<bf16_t>(float x) { return bf16_to_f32(f32_to_bf16(x)); }
+// bf16: v_cvt_pk_bf16_f32 with a zero low half leaves the rounded value in the
+// high half, i.e. already an f32 (one VALU instruction; the compiler's own
+// form rounds into the low half and shifts it up).  The compiler does not
+// insert wait states for an instruction written as inline assembly: after a
+// transcendental (v_exp_f32, v_sqrt_f32, ...) a VALU read of its result needs
+// one, so the s_nop 0 is part of the form.
+template <> __device__ __forceinline__ float rt<bf16_t>(float x) {
+    float r;
+    asm("s_nop 0\n\tv_cvt_pk_bf16_f32 %0, 0, %1" : "=v"(r) : "v"(x));
+    return r;
+}
+
+// x / d rounded to nearest as IEEE division rounds it, from r = 1 / d (one
+// correctly rounded reciprocal per divisor): q0 = x r, the remainder
+// e = x - q0 d is exact in one FMA, and q0 + e r rounded is the correctly
+// rounded quotient (Markstein's theorem for round-to-nearest binary
+// arithmetic) while d is finite and nonzero and nothing over- or underflows.
+// Three instructions instead of the division's ten; callers keep the division
+// for divisors outside that range.
+__device__ __forceinline__ float div_by(float x, float d, float r) {
+    const float q0 = x * r;
+    const float e = __builtin_fmaf(-q0, d, x);
+    return __builtin_fmaf(e, r, q0);
+}
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 

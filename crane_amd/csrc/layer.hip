@@ -112,6 +112,8 @@ __global__ __launch_bounds__(64 * kRowsPerBlock) void rms_norm_kernel(T* __restr
     }
     ss = wave_sum(ss);
     const float m = rt<T>(sqrtf(ss / (float)cols + eps));
+    const bool fast = m >= 0x1p-60f && m <= 0x1p60f;  // a normal, moderate divisor (div_by); else the division
+    const float rm = 1.0f / m;
     T* orow = out + row * cols;
 #pragma unroll
     for (int i = 0; i < CH; ++i) {
@@ -125,8 +127,13 @@ __global__ __launch_bounds__(64 * kRowsPerBlock) void rms_norm_kernel(T* __restr
 #pragma unroll
                 for (int e = 0; e < N; ++e) wv[e] = 1.f;
             }
+            if (fast) {  // uniform: x / m from the row's reciprocal (div_by)
 #pragma unroll
-            for (int e = 0; e < N; ++e) v[e] = rt<T>(v[e] / m) * wv[e];
+                for (int e = 0; e < N; ++e) v[e] = rt<T>(div_by(v[e], m, rm)) * wv[e];
+            } else {
+#pragma unroll
+                for (int e = 0; e < N; ++e) v[e] = rt<T>(v[e] / m) * wv[e];
+            }
             st16<true>(orow + idx * N, Vec<T>::pack(v));  // the pack rounds the product to T
         }
     }
@@ -180,6 +187,8 @@ __global__ __launch_bounds__(kRowThreads) void rms_norm_row_kernel(T* __restrict
 #pragma unroll
     for (int v = 1; v < kRowThreads / 64; ++v) total += part[v];
     const float m = rt<T>(sqrtf(total / (float)cols + eps));
+    const bool fast = m >= 0x1p-60f && m <= 0x1p60f;  // a normal, moderate divisor (div_by); else the division
+    const float rm = 1.0f / m;
     T* orow = out + row * cols;
 #pragma unroll
     for (int i = 0; i < CH; ++i) {
@@ -193,8 +202,13 @@ __global__ __launch_bounds__(kRowThreads) void rms_norm_row_kernel(T* __restrict
 #pragma unroll
                 for (int e = 0; e < N; ++e) wv[e] = 1.f;
             }
+            if (fast) {  // uniform: x / m from the row's reciprocal (div_by)
 #pragma unroll
-            for (int e = 0; e < N; ++e) v[e] = rt<T>(v[e] / m) * wv[e];
+                for (int e = 0; e < N; ++e) v[e] = rt<T>(div_by(v[e], m, rm)) * wv[e];
+            } else {
+#pragma unroll
+                for (int e = 0; e < N; ++e) v[e] = rt<T>(v[e] / m) * wv[e];
+            }
             st16<true>(orow + idx * N, Vec<T>::pack(v));
         }
     }
