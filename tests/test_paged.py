@@ -152,7 +152,8 @@ def test_paged_decode_long_context(gpu, orc, page_rows):
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("dtype,causal,start", [("bf16", True, [0, 0]), ("bf16", True, [200, 37]),
-                                                ("bf16", False, [64, 300]), ("f32", True, [5, 130])])
+                                                ("bf16", False, [64, 300]), ("f32", True, [5, 130]),
+                                                ("bf16", True, [1100, 700]), ("bf16", False, [1500, 900])])
 def test_paged_prefill_equals_dense(gpu, dtype, causal, start):
     import torch
     from crane_amd import ops
