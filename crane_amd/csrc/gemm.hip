@@ -6,14 +6,15 @@
 // B = x viewed as [K, M], D = y viewed as [N, M]; the bias vector (one value
 // per row of D, i.e. per output feature) is the BIAS epilogue.
 //
-// Wide skinny products (decode: M <= 32 token rows, N >= 16384 output
-// features, bf16: the merged gate_up projection and the lm_head) go to a
-// streaming kernel instead: at M = 32 the product is a stream of W through the
-// chip (2 bytes of W per 2 M flops), and it reads W closer to HBM's rate than
-// the library's tiles (measured at the Qwen3-8B decode shapes: gate_up
-// [24576, 4096] 43 us vs 47 us, lm_head [151936, 4096] 241 us vs ~355 us;
-// the narrower qkv, o_proj and down_proj shapes stay on hipBLASLt, which was
-// as fast or faster there).  The kernel:
+// Decode products (bf16, M <= 32 token rows) go to hand-written kernels
+// instead: at M = 32 the product is a stream of W through the chip (2 bytes of
+// W per 2 M flops).  Those whose K is a whole number of the per-wave rings
+// (K <= 8192; the Qwen3-8B decode step's qkv_proj, o_proj, gate_up and
+// lm_head) take the per-wave ring kernel below; other wide ones (N >= 16384)
+// the streaming kernel; the rest, down_proj among them, hipBLASLt.  The
+// streaming kernel (measured at the Qwen3-8B decode shapes before the ring
+// kernel: gate_up [24576, 4096] 43 us vs hipBLASLt's 47 us, lm_head
+// [151936, 4096] 241 us vs ~355 us):
 //  - a workgroup of 4 waves owns 64 output features and all of K; wave w
 //    multiplies features 16 w .. 16 w + 15 (the A operand of
 //    v_mfma_f32_16x16x32_bf16) by the token rows (the B operand), f32
@@ -211,6 +212,225 @@ int launch_skinny(const bf16_t* x, const bf16_t* w, const bf16_t* bias, bf16_t* 
     return launch_status(hipGetLastError());
 }
 
+// ---------------------------------------------------------------- per-wave rings
+//
+// Decode products with few token rows whose K splits into whole pipelines:
+// a workgroup owns 16 FT output features and splits K over its KS waves.  A
+// wave streams its FT x 16 W rows over its quarter (or half) of K through a
+// ring of D LDS slots of its own (buffer_load ... lds, 4 whole 256-byte row
+// pieces per 1 KiB copy, non-temporal), and reads the token rows of x for the
+// same k range straight into registers; no workgroup barrier until the end,
+// where waves 1.. KS-1 hand their f32 partial products to wave 0 through LDS
+// and wave 0 adds them in wave order (fixed, so a call's bits repeat).
+// Measured at the Qwen3-8B decode shapes (32 rows, weights rotated past the
+// Infinity Cache): o_proj [4096, 4096] 11.2 us against hipBLASLt's 13.9,
+// qkv_proj [6144, 4096] 13.6 against 15.8, gate_up [24576, 4096] 42.2 against
+// the streaming kernel's 43.0, lm_head [151936, 4096] 220 against 238.  The x
+// reads are what bounds it: without them the same kernel streams W at 5.2-6.0
+// TB/s, and x (the same bytes for every workgroup, read from L2) grows with
+// 32 token rows / 16 FT features per W byte, so wider workgroups pay less x
+// per W byte but leave CUs idle at narrow N.  The configuration follows N:
+//   N <= 4096          FT 1, KS 4, D 4 (at most 256 workgroups)
+//   4096 < N <= 8192   FT 2, KS 2, D 4, each workgroup starting its k walk
+//                      at its own stage (spreads the x reads)
+//   N > 8192           FT 4, KS 4, D 2
+// down_proj's shape [4096, 12288] stays on hipBLASLt (26.5 us against 29.1).
+
+constexpr int kRingMaxK = 8192;
+
+template <int N>
+__device__ __forceinline__ void vm_wait() {
+    __builtin_amdgcn_s_waitcnt(0x0F70 | (N & 15) | ((N >> 4) << 14));
+}
+
+// Wait until at most `stages` later stages' loads (P loads each) are in
+// flight; `stages` is a compile-time constant after unrolling.
+template <int P>
+__device__ __forceinline__ void vm_wait_stages(int stages) {
+    switch (stages) {
+        case 0: vm_wait<0>(); break;
+        case 1: vm_wait<P>(); break;
+        case 2: vm_wait<2 * P>(); break;
+        default: vm_wait<3 * P>(); break;
+    }
+}
+
+// One stage of a wave's W rows into its ring slot: n copies of 1 KiB (4 rows
+// x 256 bytes each), non-temporal.  (Not a template: the host pass cannot
+// form the LDS pointer the copy takes.)
+__device__ __forceinline__ void ring_copy(__amdgpu_buffer_rsrc_t src, uint8_t* dst, const uint32_t* vofs, int n,
+                                          int soff) {
+    for (int c = 0; c < n; ++c) __builtin_amdgcn_raw_ptr_buffer_load_lds(src, dst + c * 1024, 16, vofs[c], soff, 0, 2);
+}
+
+// y = x[M, K] W[N, K]^T (+ b), M <= 16 MT: N / (16 FT) workgroups of 64 KS
+// threads.  Wave w covers k in [w K / KS, (w + 1) K / KS) in stages of 128
+// (nst = K / (128 KS), a multiple of D and at least D); stage s of it lives in
+// ring slot s % D, D - 1 stages in flight.  Lane l holds A row l % 16 (feature
+// 16 f + l % 16 of the workgroup's FT tiles) and B column l % 16 (token
+// 16 m + l % 16) with 8 k elements of chunk (l / 16 + 4 i) of a stage's 256
+// bytes in k-step i: A and B take the same k order, so the sum is the dot
+// product.  Token rows past M read row M - 1 (their columns are not stored).
+template <int MT, int KS, int D, int FT, bool ROT>
+__global__ __launch_bounds__(64 * KS) void ring_gemm_kernel(const bf16_t* __restrict__ x, const bf16_t* __restrict__ w,
+                                                            const bf16_t* __restrict__ bias, bf16_t* __restrict__ y,
+                                                            int M, int N, int K) {
+    constexpr int kLoads = 4 * FT + 4 * MT;  // loads per stage: W copies, then x fragments
+    static_assert(D >= 2 && D <= 4, "ring depth");
+    static_assert((D - 1) * kLoads <= 63, "the loads in flight fit the 6-bit vmcnt");
+    __shared__ f32x4_v part[KS > 1 ? KS - 1 : 1][FT][MT][64];
+    // one LDS object per (ring slot, feature tile): the compiler's wait-count
+    // pass then tells the copies in flight apart from the rows being read
+#define CRANE_RING_SLOT(d, f) \
+    __shared__ __attribute__((aligned(1024))) uint8_t ring##d##f[D > d && FT > f ? KS : 1][4096];
+    CRANE_RING_SLOT(0, 0) CRANE_RING_SLOT(0, 1) CRANE_RING_SLOT(0, 2) CRANE_RING_SLOT(0, 3)
+    CRANE_RING_SLOT(1, 0) CRANE_RING_SLOT(1, 1) CRANE_RING_SLOT(1, 2) CRANE_RING_SLOT(1, 3)
+    CRANE_RING_SLOT(2, 0) CRANE_RING_SLOT(2, 1) CRANE_RING_SLOT(2, 2) CRANE_RING_SLOT(2, 3)
+    CRANE_RING_SLOT(3, 0) CRANE_RING_SLOT(3, 1) CRANE_RING_SLOT(3, 2) CRANE_RING_SLOT(3, 3)
+#undef CRANE_RING_SLOT
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    // slot d's rows of feature tile f (d, f compile-time constants after unrolling)
+    auto slot = [&](int d, int f) -> uint8_t* {
+        const int wv = D > d && FT > f ? wave : 0;
+        switch (4 * d + f) {
+            case 0: return ring00[wv]; case 1: return ring01[wv]; case 2: return ring02[wv]; case 3: return ring03[wv];
+            case 4: return ring10[wv]; case 5: return ring11[wv]; case 6: return ring12[wv]; case 7: return ring13[wv];
+            case 8: return ring20[wv]; case 9: return ring21[wv]; case 10: return ring22[wv]; case 11: return ring23[wv];
+            case 12: return ring30[wv]; case 13: return ring31[wv]; case 14: return ring32[wv]; default: return ring33[wv];
+        }
+    };
+    const int tile = blockIdx.x;
+    const int kw = K / KS, k0 = wave * kw, nst = kw / 128;
+    const int r = lane & 15, g = lane >> 4;
+    // the W resource spans the workgroup's rows from this wave's k0
+    const __amdgpu_buffer_rsrc_t src = sk_rsrc(w + (int64_t)tile * 16 * FT * K + k0, (uint32_t)16 * FT * K * 2);
+    uint32_t vofs[4 * FT];
+#pragma unroll
+    for (int c = 0; c < 4 * FT; ++c) {
+        const int row = 4 * c + (lane >> 4), sl = lane & 15;
+        vofs[c] = (uint32_t)row * K * 2 + 16u * (sl ^ (row & 15));  // chunk sl ^ (row & 15) lands in slot sl
+    }
+    const bf16_t* xp[MT];
+#pragma unroll
+    for (int m = 0; m < MT; ++m) xp[m] = x + (int64_t)min(16 * m + r, M - 1) * K + k0 + 8 * g;
+    const int rot = ROT ? tile % nst : 0;
+    uint4 xb[D][MT][4];
+    f32x4_v acc[FT][MT];
+#pragma unroll
+    for (int f = 0; f < FT; ++f)
+#pragma unroll
+        for (int m = 0; m < MT; ++m) acc[f][m] = f32x4_v{};
+    auto load = [&](int d, int s) {
+        if (ROT) {
+            s += rot;
+            if (s >= nst) s -= nst;
+        }
+#pragma unroll
+        for (int f = 0; f < FT; ++f) ring_copy(src, slot(d, f), vofs + 4 * f, 4, s * 256);
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int m = 0; m < MT; ++m) xb[d][m][i] = *reinterpret_cast<const uint4*>(xp[m] + s * 128 + 32 * i);
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    // multiply the stage in slot d once its loads have landed (`later` later
+    // stages' loads may stay in flight)
+    auto mul = [&](int d, int later) {
+        vm_wait_stages<kLoads>(later);
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");  // keeps the LDS reads below the wait
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int f = 0; f < FT; ++f) {
+                const uint4 a = *reinterpret_cast<const uint4*>(slot(d, f) + r * 256 + 16 * ((g + 4 * i) ^ r));
+#pragma unroll
+                for (int m = 0; m < MT; ++m)
+                    acc[f][m] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a), as_bf16x8(xb[d][m][i]), acc[f][m],
+                                                                        0, 0, 0);
+            }
+        __builtin_amdgcn_sched_barrier(0);
+    };
+#pragma unroll
+    for (int d = 0; d < D - 1; ++d) load(d, d);
+    for (int s = 0; s + D < nst; s += D) {
+#pragma unroll
+        for (int d = 0; d < D; ++d) {
+            load((d + D - 1) % D, s + d + D - 1);
+            mul(d, D - 1);
+        }
+    }
+    load(D - 1, nst - 1);
+    mul(0, D - 1);
+#pragma unroll
+    for (int d = 1; d < D; ++d) mul(d, D - 1 - d);
+    if (KS > 1) {
+        if (wave > 0)
+#pragma unroll
+            for (int f = 0; f < FT; ++f)
+#pragma unroll
+                for (int m = 0; m < MT; ++m) part[wave - 1][f][m][lane] = acc[f][m];
+        __syncthreads();
+        if (wave > 0) return;
+#pragma unroll
+        for (int j = 0; j < KS - 1; ++j)
+#pragma unroll
+            for (int f = 0; f < FT; ++f)
+#pragma unroll
+                for (int m = 0; m < MT; ++m) acc[f][m] += part[j][f][m][lane];
+    }
+#pragma unroll
+    for (int f = 0; f < FT; ++f) {
+        const int n = (tile * FT + f) * 16 + 4 * g;
+#pragma unroll
+        for (int m = 0; m < MT; ++m) {
+            const int t = 16 * m + r;
+            if (t >= M) continue;
+            float v[4] = {acc[f][m][0], acc[f][m][1], acc[f][m][2], acc[f][m][3]};
+            if (bias) {
+                float bv[4];
+                load4(bias + n, bv);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) v[e] += bv[e];
+            }
+            store4(y + (int64_t)t * N + n, v);
+        }
+    }
+}
+
+// The ring configuration for a shape: features per workgroup (16 FT), waves
+// (KS) and ring depth (D); 0 when the shape does not take the ring kernel.
+struct RingCfg {
+    int ft, ks, d;
+};
+
+RingCfg ring_cfg(int64_t M, int64_t N, int64_t K) {
+    if (M < 1 || M > kSkMaxM || K < 1 || K > kRingMaxK || N < 1 || N > 0x7fffffff) return {0, 0, 0};
+    const RingCfg c = N <= 4096 ? RingCfg{1, 4, 4} : (N <= 8192 ? RingCfg{2, 2, 4} : RingCfg{4, 4, 2});
+    if (N % (16 * c.ft) || K % (128 * c.ks * c.d)) return {0, 0, 0};
+    return c;
+}
+
+template <int MT>
+void launch_ring_mt(const RingCfg& c, const bf16_t* x, const bf16_t* w, const bf16_t* bias, bf16_t* y, int M, int N,
+                    int K, hipStream_t st) {
+    const dim3 grid((unsigned)(N / (16 * c.ft))), block(64 * c.ks);
+    if (c.ft == 1)
+        hipLaunchKernelGGL((ring_gemm_kernel<MT, 4, 4, 1, false>), grid, block, 0, st, x, w, bias, y, M, N, K);
+    else if (c.ft == 2)
+        hipLaunchKernelGGL((ring_gemm_kernel<MT, 2, 4, 2, true>), grid, block, 0, st, x, w, bias, y, M, N, K);
+    else
+        hipLaunchKernelGGL((ring_gemm_kernel<MT, 4, 2, 4, false>), grid, block, 0, st, x, w, bias, y, M, N, K);
+}
+
+int launch_ring(const RingCfg& c, const bf16_t* x, const bf16_t* w, const bf16_t* bias, bf16_t* y, int M, int N, int K,
+                hipStream_t st) {
+    if (M <= 16)
+        launch_ring_mt<1>(c, x, w, bias, y, M, N, K, st);
+    else
+        launch_ring_mt<2>(c, x, w, bias, y, M, N, K, st);
+    return launch_status(hipGetLastError());
+}
+
 struct Plan {
     hipblasLtMatmulDesc_t desc = nullptr;
     hipblasLtMatrixLayout_t a = nullptr, b = nullptr, d = nullptr;
@@ -253,6 +473,12 @@ class Gemm {
     int linear(const void* x, const void* w, const void* bias, void* y, int64_t M, int64_t N, int64_t K, int dtype,
                hipStream_t st) {
         std::lock_guard<std::mutex> lock(mu_);
+        if (dtype == CRANE_HIP_BF16) {
+            const RingCfg rc = ring_cfg(M, N, K);
+            if (rc.ft)
+                return launch_ring(rc, (const bf16_t*)x, (const bf16_t*)w, (const bf16_t*)bias, (bf16_t*)y, (int)M,
+                                   (int)N, (int)K, st);
+        }
         if (dtype == CRANE_HIP_BF16 && skinny_fits(M, N, K))
             return launch_skinny((const bf16_t*)x, (const bf16_t*)w, (const bf16_t*)bias, (bf16_t*)y, (int)M, (int)N,
                                  (int)K, st);

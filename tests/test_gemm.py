@@ -103,7 +103,7 @@ def test_linear_parity(gpu, orc, dtype, M, N, K, bias):
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("M,N,K,bias", [
-    (32, 16384, 1024, False),  # the decode batch of config 3; 8 stages of 128
+    (32, 16384, 1152, False),  # the decode batch of config 3; 9 stages of 128
     (17, 16448, 384, True),    # a partial second token group; 3 stages; 257 workgroups
     (8, 16384, 640, True),     # 5 stages: the unrolled-by-three loop's remainder of 2
     (1, 16384, 256, True),     # one token row; 2 stages
@@ -111,13 +111,42 @@ def test_linear_parity(gpu, orc, dtype, M, N, K, bias):
 ])
 def test_linear_streaming_parity(gpu, orc, M, N, K, bias):
     """Wide bf16 products with few token rows run the streaming kernel
-    (M <= 32, N >= 16384, K a multiple of 128), the gate_up and lm_head shapes
-    of a decode step; same bar as the library path."""
+    (M <= 32, N >= 16384, K a multiple of 128) when K is not a whole number of
+    the per-wave ring kernel's pipelines (K % 1024 != 0 here); same bar as
+    the library path."""
     from crane_amd import ops
     print(f"linear (streaming) M={M} N={N} K={K} bias={bias}", flush=True)
     x, w, b = _case(900 + M + K, M, N, K, "bf16", bias)
     got = ops.linear(_t(x, "bf16", gpu), _t(w, "bf16", gpu), _t(b, "bf16", gpu) if bias else None)
     assert_linear_close(got.float().cpu().numpy(), x, w, b, "bf16", orc, f"streaming linear {M}x{N}x{K}")
+    got2 = ops.linear(_t(x, "bf16", gpu), _t(w, "bf16", gpu), _t(b, "bf16", gpu) if bias else None)
+    assert bool((got == got2).all())
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("M,N,K,bias", [
+    (32, 4096, 4096, False),   # o_proj at the c3 decode batch: 16 features x 4 waves, 2 stages ahead
+    (5, 4096, 2048, True),     # one token group; each wave's 4 stages fill the ring once (no loop trip)
+    (3, 2048, 6144, True),     # 128 workgroups; 12 stages a wave
+    (32, 6144, 4096, True),    # qkv_proj at c3: 32 features x 2 waves, rotated k walk (16 stages)
+    (17, 8192, 1024, False),   # a partial second token group; 4 stages a wave, rotation over 4
+    (32, 24576, 1024, True),   # gate_up-like: 64 features x 4 waves, 2-slot ring
+    (1, 12288, 2048, False),   # one token row, wide
+    (32, 4096, 12288, False),  # down_proj's shape: K past the ring kernel's limit, hipBLASLt
+])
+def test_linear_ring_parity(gpu, orc, M, N, K, bias):
+    """bf16 products with M <= 32 token rows, N a multiple of the workgroup's
+    16/32/64 features (N <= 4096 / <= 8192 / wider) and K <= 8192 a whole
+    number of the per-wave rings (K % 2048 == 0 for the narrowest, 1024 for
+    the others) run the per-wave ring kernel: the decode step's qkv_proj,
+    o_proj, gate_up and lm_head.  Same bar as the library path, and a second
+    call repeats the bits (the waves' partial products are added in a fixed
+    order)."""
+    from crane_amd import ops
+    print(f"linear (ring) M={M} N={N} K={K} bias={bias}", flush=True)
+    x, w, b = _case(1300 + M + N // 64 + K, M, N, K, "bf16", bias)
+    got = ops.linear(_t(x, "bf16", gpu), _t(w, "bf16", gpu), _t(b, "bf16", gpu) if bias else None)
+    assert_linear_close(got.float().cpu().numpy(), x, w, b, "bf16", orc, f"ring linear {M}x{N}x{K}")
     got2 = ops.linear(_t(x, "bf16", gpu), _t(w, "bf16", gpu), _t(b, "bf16", gpu) if bias else None)
     assert bool((got == got2).all())
 
