@@ -302,10 +302,10 @@ def bench_layer(args, dev, stream, lib):
 def bench_gemm(args, dev, stream, lib):
     """The projections (include/crane_gemm.h): Qwen2.5-7B qkv_proj (with bias)
     and o_proj at config 4's 8 x 4096 rows (hipBLASLt), and at config 3's 32
-    decode rows the Qwen3-8B qkv_proj (hipBLASLt), gate_up and lm_head (the
-    streaming kernel).  The decode shapes rotate over enough weight copies
-    (> 600 MB) that every launch streams its weight from HBM, not from the
-    256 MB Infinity Cache."""
+    decode rows the Qwen3-8B qkv_proj, o_proj, gate_up and lm_head (the
+    per-wave ring kernel) and down_proj (hipBLASLt).  The decode shapes rotate
+    over enough weight copies (> 600 MB) that every launch streams its weight
+    from HBM, not from the 256 MB Infinity Cache."""
     import ctypes
     import torch
     h = ctypes.c_void_p()
@@ -314,7 +314,8 @@ def bench_gemm(args, dev, stream, lib):
     st = stream.cuda_stream
     res = {}
     for tag, M, N, K, bias in (("c4_qkv_proj", 8 * 4096, 4608, 3584, True), ("c4_o_proj", 8 * 4096, 3584, 3584, False),
-                               ("c3_qkv_proj", 32, 6144, 4096, False), ("c3_gate_up", 32, 24576, 4096, False),
+                               ("c3_qkv_proj", 32, 6144, 4096, False), ("c3_o_proj", 32, 4096, 4096, False),
+                               ("c3_gate_up", 32, 24576, 4096, False), ("c3_down_proj", 32, 4096, 12288, False),
                                ("c3_lm_head", 32, 151936, 4096, False)):
         gen = torch.Generator(device=dev).manual_seed(SEED0 + 9)
         x = randn((M, K), gen, torch.bfloat16, dev)
