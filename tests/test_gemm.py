@@ -2,7 +2,7 @@
 y = x W^T + b -- Crane's merged qkv_proj, whose rows feed the fused append
 (qwen3/modeling.rs:382-387; with the Qwen2.5 bias, qwen25/qwen2.rs:136-138),
 o_proj (:466, :502), the MLP projections and the lm_head; on hipBLASLt, or on
-the streaming kernel for wide decode-shaped bf16 products.
+the per-wave ring and streaming kernels for decode-shaped bf16 products.
 
 The oracle's linear is pinned to numpy float64 matmul (a transposed weight
 fails); the GPU is held to the oracle within the rounding bound of its two
@@ -10,6 +10,7 @@ differences (f32 accumulation in another order, and one rounding of product
 + bias where candle rounds twice) and the mean-relative bar, with weights
 scaled like trained ones (std 1/sqrt(K)) so outputs are O(1)."""
 import math
+import os
 
 import numpy as np
 import pytest
@@ -147,6 +148,49 @@ def test_linear_ring_parity(gpu, orc, M, N, K, bias):
     x, w, b = _case(1300 + M + N // 64 + K, M, N, K, "bf16", bias)
     got = ops.linear(_t(x, "bf16", gpu), _t(w, "bf16", gpu), _t(b, "bf16", gpu) if bias else None)
     assert_linear_close(got.float().cpu().numpy(), x, w, b, "bf16", orc, f"ring linear {M}x{N}x{K}")
+    got2 = ops.linear(_t(x, "bf16", gpu), _t(w, "bf16", gpu), _t(b, "bf16", gpu) if bias else None)
+    assert bool((got == got2).all())
+
+
+N_RANDOM = int(os.environ.get("CRANE_RANDOM_GEMM", 12))
+SEED = int(os.environ.get("CRANE_RANDOM_SEED", 0))
+
+
+def linear_draw(seed: int, i: int):
+    """Draw i of the randomised decode-projection sweep: (M, N, K, bias) with
+    1-32 token rows, cycling over the shapes each path takes -- the ring
+    kernel's three configurations (N <= 4096, <= 8192, wider), the streaming
+    kernel (N >= 16384, K not a multiple of 1024) and hipBLASLt (anything
+    else) -- and M N K at most 1.5e9 so the oracle finishes in seconds."""
+    r = cases.rng(seed + 9100 + i)
+    M = int(r.integers(1, 33))
+    kind = i % 5
+    if kind == 0:
+        N, K = 16 * int(r.integers(1, 257)), 2048 * int(r.integers(1, 5))
+    elif kind == 1:
+        N, K = 32 * int(r.integers(129, 257)), 1024 * int(r.integers(1, 9))
+    elif kind == 2:
+        N, K = 64 * int(r.integers(129, 1025)), 1024 * int(r.integers(1, 5))
+    elif kind == 3:
+        N, K = 64 * int(r.integers(256, 513)), 128 * int(r.choice([1, 3, 5, 7, 9, 11, 13]))
+    else:
+        N, K = int(r.integers(1, 3000)), int(r.integers(1, 1500))
+    while M * N * K > 1.5e9 and K > 1024:
+        K -= 1024
+    return M, N, K, bool(r.random() < 0.5)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("i", range(N_RANDOM))
+def test_random_decode_linear(gpu, orc, i):
+    """Random decode-shaped bf16 products against the oracle (same bar as the
+    fixed shapes), each repeated for identical bits."""
+    from crane_amd import ops
+    M, N, K, bias = linear_draw(SEED, i)
+    print(f"random linear {i} (seed {SEED}): M={M} N={N} K={K} bias={bias}", flush=True)
+    x, w, b = _case(SEED + 9200 + i, M, N, K, "bf16", bias)
+    got = ops.linear(_t(x, "bf16", gpu), _t(w, "bf16", gpu), _t(b, "bf16", gpu) if bias else None)
+    assert_linear_close(got.float().cpu().numpy(), x, w, b, "bf16", orc, f"random linear {M}x{N}x{K}")
     got2 = ops.linear(_t(x, "bf16", gpu), _t(w, "bf16", gpu), _t(b, "bf16", gpu) if bias else None)
     assert bool((got == got2).all())
 
