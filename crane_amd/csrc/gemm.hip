@@ -224,7 +224,7 @@ int launch_skinny(const bf16_t* x, const bf16_t* w, const bf16_t* bias, bf16_t* 
 // and wave 0 adds them in wave order (fixed, so a call's bits repeat).
 // Measured at the Qwen3-8B decode shapes (32 rows, weights rotated past the
 // Infinity Cache): o_proj [4096, 4096] 11.2 us against hipBLASLt's 13.9,
-// qkv_proj [6144, 4096] 13.6 against 15.8, gate_up [24576, 4096] 42.2 against
+// qkv_proj [6144, 4096] 13.6 against 15.8, gate_up [24576, 4096] 36.7 against
 // the streaming kernel's 43.0, lm_head [151936, 4096] 220 against 238.  The x
 // reads are what bounds it: without them the same kernel streams W at 5.2-6.0
 // TB/s, and x (the same bytes for every workgroup, read from L2) grows with
@@ -233,7 +233,10 @@ int launch_skinny(const bf16_t* x, const bf16_t* w, const bf16_t* bias, bf16_t* 
 //   N <= 4096          FT 1, KS 4, D 4 (at most 256 workgroups)
 //   4096 < N <= 8192   FT 2, KS 2, D 4, each workgroup starting its k walk
 //                      at its own stage (spreads the x reads)
-//   N > 8192           FT 4, KS 4, D 2
+//   N > 8192           FT 4 or 3, KS 4, D 2: one workgroup per CU (LDS), and
+//                      FT 3 where it evens out the CUs' shares (gate_up:
+//                      512 workgroups of 48 features, 36.7 us, against 384 of
+//                      64, 42.2 us, two rounds either way)
 // down_proj's shape [4096, 12288] stays on hipBLASLt (26.5 us against 29.1).
 
 constexpr int kRingMaxK = 8192;
@@ -403,9 +406,18 @@ struct RingCfg {
     int ft, ks, d;
 };
 
+// Wide N: 48 or 64 features a workgroup (one workgroup per CU by LDS), the one
+// whose busiest CU streams the fewest 16-feature tiles, i.e. the least
+// ceil(workgroups / 256) * FT; 64 on a tie (less x per W byte).
+constexpr int kRingCUs = 256;
+
 RingCfg ring_cfg(int64_t M, int64_t N, int64_t K) {
     if (M < 1 || M > kSkMaxM || K < 1 || K > kRingMaxK || N < 1 || N > 0x7fffffff) return {0, 0, 0};
-    const RingCfg c = N <= 4096 ? RingCfg{1, 4, 4} : (N <= 8192 ? RingCfg{2, 2, 4} : RingCfg{4, 4, 2});
+    RingCfg c = N <= 4096 ? RingCfg{1, 4, 4} : (N <= 8192 ? RingCfg{2, 2, 4} : RingCfg{4, 4, 2});
+    if (c.ft == 4 && N % 48 == 0) {
+        auto load = [&](int64_t ft) { return (N / (16 * ft) + kRingCUs - 1) / kRingCUs * ft; };
+        if (N % 64 != 0 || load(3) < load(4)) c = RingCfg{3, 4, 2};
+    }
     if (N % (16 * c.ft) || K % (128 * c.ks * c.d)) return {0, 0, 0};
     return c;
 }
@@ -418,6 +430,8 @@ void launch_ring_mt(const RingCfg& c, const bf16_t* x, const bf16_t* w, const bf
         hipLaunchKernelGGL((ring_gemm_kernel<MT, 4, 4, 1, false>), grid, block, 0, st, x, w, bias, y, M, N, K);
     else if (c.ft == 2)
         hipLaunchKernelGGL((ring_gemm_kernel<MT, 2, 4, 2, true>), grid, block, 0, st, x, w, bias, y, M, N, K);
+    else if (c.ft == 3)
+        hipLaunchKernelGGL((ring_gemm_kernel<MT, 4, 2, 3, false>), grid, block, 0, st, x, w, bias, y, M, N, K);
     else
         hipLaunchKernelGGL((ring_gemm_kernel<MT, 4, 2, 4, false>), grid, block, 0, st, x, w, bias, y, M, N, K);
 }

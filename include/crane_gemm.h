@@ -16,10 +16,10 @@
  * the sum), except bf16 products with few token rows (M <= 32), which
  * hand-written kernels run with the same accumulation and rounding: a per-wave
  * ring kernel when K <= 8192 splits into its pipelines (K a multiple of 2048
- * for N <= 4096, of 1024 above; N a multiple of 16, 32 or 64 features for
- * N <= 4096, <= 8192 or wider: the decode step's qkv_proj, o_proj, gate_up and
- * lm_head), else a streaming kernel for N >= 16384 (N a multiple of 64, K of
- * 128).  A crane_gemm context holds the hipBLASLt handle,
+ * for N <= 4096, of 1024 above; N a multiple of 16, 32, or 48 or 64 features
+ * for N <= 4096, <= 8192 or wider: the decode step's qkv_proj, o_proj, gate_up
+ * and lm_head), else a streaming kernel for N >= 16384 (N a multiple of 64, K
+ * of 128).  A crane_gemm context holds the hipBLASLt handle,
  * a workspace allocated at creation and the algorithm chosen for each shape
  * (the heuristic query runs once per shape).  Conventions otherwise as in
  * crane_hip.h; crane_gemm_linear does not allocate or synchronise.  Calls on

@@ -131,13 +131,15 @@ def test_linear_streaming_parity(gpu, orc, M, N, K, bias):
     (3, 2048, 6144, True),     # 128 workgroups; 12 stages a wave
     (32, 6144, 4096, True),    # qkv_proj at c3: 32 features x 2 waves, rotated k walk (16 stages)
     (17, 8192, 1024, False),   # a partial second token group; 4 stages a wave, rotation over 4
-    (32, 24576, 1024, True),   # gate_up-like: 64 features x 4 waves, 2-slot ring
-    (1, 12288, 2048, False),   # one token row, wide
+    (32, 24576, 1024, True),   # gate_up's N: 48 features x 4 waves (512 workgroups, two per CU), 2-slot ring
+    (32, 16384, 2048, True),   # 64 features x 4 waves (256 workgroups)
+    (9, 9072, 1024, False),    # N a multiple of 48, not of 64: 48 features
+    (1, 12288, 2048, False),   # one token row, wide (48 features: 256 workgroups)
     (32, 4096, 12288, False),  # down_proj's shape: K past the ring kernel's limit, hipBLASLt
 ])
 def test_linear_ring_parity(gpu, orc, M, N, K, bias):
     """bf16 products with M <= 32 token rows, N a multiple of the workgroup's
-    16/32/64 features (N <= 4096 / <= 8192 / wider) and K <= 8192 a whole
+    16/32/48 or 64 features (N <= 4096 / <= 8192 / wider) and K <= 8192 a whole
     number of the per-wave rings (K % 2048 == 0 for the narrowest, 1024 for
     the others) run the per-wave ring kernel: the decode step's qkv_proj,
     o_proj, gate_up and lm_head.  Same bar as the library path, and a second
