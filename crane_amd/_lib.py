@@ -83,6 +83,8 @@ SIGNATURES = {
     "crane_gemm_create": ([_sz, _vpp], _i),
     "crane_gemm_destroy": ([_vp], None),
     "crane_gemm_linear": ([_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i, _vp], _i),
+    "crane_gemm_silu_mul_supported": ([_i64, _i64, _i64, _i], _i),
+    "crane_gemm_linear_silu_mul": ([_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i, _vp], _i),
     # include/crane_pkv.h
     "crane_pkv_create": ([_i, _i, _i, _i, _i64, _i, _i, _vpp], _i),
     "crane_pkv_destroy": ([_vp], None),

@@ -34,6 +34,11 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
     return __builtin_bit_cast(uint32_t, v);
 }
 
+// Crane's SiLU, g / (1 + exp(-g)) in f32 (fused_ops.cu:104-126): one
+// definition for the row kernel and the gated GEMM epilogue, so both round
+// the same value.
+__device__ __forceinline__ float silu(float g) { return g / (1.0f + expf(-g)); }
+
 // Element type traits: f32 and bf16 storage, f32 arithmetic.
 template <typename T> struct Elem;
 template <> struct Elem<float> {

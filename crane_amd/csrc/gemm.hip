@@ -274,42 +274,56 @@ __device__ __forceinline__ void ring_copy(__amdgpu_buffer_rsrc_t src, uint8_t* d
 // 16 m + l % 16) with 8 k elements of chunk (l / 16 + 4 i) of a stage's 256
 // bytes in k-step i: A and B take the same k order, so the sum is the dot
 // product.  Token rows past M read row M - 1 (their columns are not stored).
-template <int MT, int KS, int D, int FT, bool ROT>
+// GATED: W is a merged gate_up [2 I, K] (N = 2 I rows) and y = T(silu(T(g))
+// T(u)) [M, I]: the workgroup's first FT / 2 tiles are gate rows
+// [8 FT tile, +8 FT), the others the up rows I + 8 FT tile .. of the same
+// features, so each lane holds the gate and up sums of the same outputs.
+template <int MT, int KS, int D, int FT, bool ROT, bool GATED>
 __global__ __launch_bounds__(64 * KS) void ring_gemm_kernel(const bf16_t* __restrict__ x, const bf16_t* __restrict__ w,
                                                             const bf16_t* __restrict__ bias, bf16_t* __restrict__ y,
                                                             int M, int N, int K) {
     constexpr int kLoads = 4 * FT + 4 * MT;  // loads per stage: W copies, then x fragments
-    static_assert(D >= 2 && D <= 4, "ring depth");
+    constexpr int H = GATED ? FT / 2 : FT;   // tiles per W row range
+    static_assert(D >= 2 && D <= 4 && FT >= 1 && FT <= 6, "ring depth and width");
+    static_assert(!GATED || FT % 2 == 0, "gated tiles come in gate / up pairs");
     static_assert((D - 1) * kLoads <= 63, "the loads in flight fit the 6-bit vmcnt");
     __shared__ f32x4_v part[KS > 1 ? KS - 1 : 1][FT][MT][64];
     // one LDS object per (ring slot, feature tile): the compiler's wait-count
     // pass then tells the copies in flight apart from the rows being read
 #define CRANE_RING_SLOT(d, f) \
     __shared__ __attribute__((aligned(1024))) uint8_t ring##d##f[D > d && FT > f ? KS : 1][4096];
-    CRANE_RING_SLOT(0, 0) CRANE_RING_SLOT(0, 1) CRANE_RING_SLOT(0, 2) CRANE_RING_SLOT(0, 3)
-    CRANE_RING_SLOT(1, 0) CRANE_RING_SLOT(1, 1) CRANE_RING_SLOT(1, 2) CRANE_RING_SLOT(1, 3)
-    CRANE_RING_SLOT(2, 0) CRANE_RING_SLOT(2, 1) CRANE_RING_SLOT(2, 2) CRANE_RING_SLOT(2, 3)
-    CRANE_RING_SLOT(3, 0) CRANE_RING_SLOT(3, 1) CRANE_RING_SLOT(3, 2) CRANE_RING_SLOT(3, 3)
+#define CRANE_RING_SLOTS(d) \
+    CRANE_RING_SLOT(d, 0) CRANE_RING_SLOT(d, 1) CRANE_RING_SLOT(d, 2) CRANE_RING_SLOT(d, 3) CRANE_RING_SLOT(d, 4) \
+    CRANE_RING_SLOT(d, 5)
+    CRANE_RING_SLOTS(0) CRANE_RING_SLOTS(1) CRANE_RING_SLOTS(2) CRANE_RING_SLOTS(3)
+#undef CRANE_RING_SLOTS
 #undef CRANE_RING_SLOT
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     // slot d's rows of feature tile f (d, f compile-time constants after unrolling)
     auto slot = [&](int d, int f) -> uint8_t* {
         const int wv = D > d && FT > f ? wave : 0;
-        switch (4 * d + f) {
-            case 0: return ring00[wv]; case 1: return ring01[wv]; case 2: return ring02[wv]; case 3: return ring03[wv];
-            case 4: return ring10[wv]; case 5: return ring11[wv]; case 6: return ring12[wv]; case 7: return ring13[wv];
-            case 8: return ring20[wv]; case 9: return ring21[wv]; case 10: return ring22[wv]; case 11: return ring23[wv];
-            case 12: return ring30[wv]; case 13: return ring31[wv]; case 14: return ring32[wv]; default: return ring33[wv];
+        switch (6 * d + f) {
+            case 0: return ring00[wv]; case 1: return ring01[wv]; case 2: return ring02[wv];
+            case 3: return ring03[wv]; case 4: return ring04[wv]; case 5: return ring05[wv];
+            case 6: return ring10[wv]; case 7: return ring11[wv]; case 8: return ring12[wv];
+            case 9: return ring13[wv]; case 10: return ring14[wv]; case 11: return ring15[wv];
+            case 12: return ring20[wv]; case 13: return ring21[wv]; case 14: return ring22[wv];
+            case 15: return ring23[wv]; case 16: return ring24[wv]; case 17: return ring25[wv];
+            case 18: return ring30[wv]; case 19: return ring31[wv]; case 20: return ring32[wv];
+            case 21: return ring33[wv]; case 22: return ring34[wv]; default: return ring35[wv];
         }
     };
     const int tile = blockIdx.x;
     const int kw = K / KS, k0 = wave * kw, nst = kw / 128;
     const int r = lane & 15, g = lane >> 4;
-    // the W resource spans the workgroup's rows from this wave's k0
-    const __amdgpu_buffer_rsrc_t src = sk_rsrc(w + (int64_t)tile * 16 * FT * K + k0, (uint32_t)16 * FT * K * 2);
-    uint32_t vofs[4 * FT];
+    // The W resources span the workgroup's rows from this wave's k0: its 16 H
+    // rows (GATED: the gate rows, and the up rows N / 2 further).
+    const int64_t row0 = (int64_t)tile * 16 * H;
+    const __amdgpu_buffer_rsrc_t src_lo = sk_rsrc(w + row0 * K + k0, (uint32_t)16 * H * K * 2);
+    const __amdgpu_buffer_rsrc_t src_hi = sk_rsrc(w + (row0 + (GATED ? N / 2 : 0)) * K + k0, (uint32_t)16 * H * K * 2);
+    uint32_t vofs[4 * H];
 #pragma unroll
-    for (int c = 0; c < 4 * FT; ++c) {
+    for (int c = 0; c < 4 * H; ++c) {
         const int row = 4 * c + (lane >> 4), sl = lane & 15;
         vofs[c] = (uint32_t)row * K * 2 + 16u * (sl ^ (row & 15));  // chunk sl ^ (row & 15) lands in slot sl
     }
@@ -329,7 +343,8 @@ __global__ __launch_bounds__(64 * KS) void ring_gemm_kernel(const bf16_t* __rest
             if (s >= nst) s -= nst;
         }
 #pragma unroll
-        for (int f = 0; f < FT; ++f) ring_copy(src, slot(d, f), vofs + 4 * f, 4, s * 256);
+        for (int f = 0; f < FT; ++f)
+            ring_copy(f < H ? src_lo : src_hi, slot(d, f), vofs + 4 * (f < H ? f : f - H), 4, s * 256);
 #pragma unroll
         for (int i = 0; i < 4; ++i)
 #pragma unroll
@@ -381,6 +396,24 @@ __global__ __launch_bounds__(64 * KS) void ring_gemm_kernel(const bf16_t* __rest
 #pragma unroll
                 for (int m = 0; m < MT; ++m) acc[f][m] += part[j][f][m][lane];
     }
+    if (GATED) {
+        const int I = N / 2;
+#pragma unroll
+        for (int f = 0; f < H; ++f) {
+            const int n = (tile * H + f) * 16 + 4 * g;
+#pragma unroll
+            for (int m = 0; m < MT; ++m) {
+                const int t = 16 * m + r;
+                if (t >= M) continue;
+                float v[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e)  // gate_up rounded to T, then Crane's silu * up rounded once
+                    v[e] = silu(bf16_to_f32(f32_to_bf16(acc[f][m][e]))) * bf16_to_f32(f32_to_bf16(acc[f + H][m][e]));
+                store4(y + (int64_t)t * I + n, v);
+            }
+        }
+        return;
+    }
 #pragma unroll
     for (int f = 0; f < FT; ++f) {
         const int n = (tile * FT + f) * 16 + 4 * g;
@@ -403,45 +436,60 @@ __global__ __launch_bounds__(64 * KS) void ring_gemm_kernel(const bf16_t* __rest
 // The ring configuration for a shape: features per workgroup (16 FT), waves
 // (KS) and ring depth (D); 0 when the shape does not take the ring kernel.
 struct RingCfg {
-    int ft, ks, d;
+    int ft, ks, d;  // features / 16 per workgroup, waves, ring depth; ft == 0: not taken
 };
 
-// Wide N: 48 or 64 features a workgroup (one workgroup per CU by LDS), the one
-// whose busiest CU streams the fewest 16-feature tiles, i.e. the least
-// ceil(workgroups / 256) * FT; 64 on a tie (less x per W byte).
+// Wide N (> 8192): one workgroup per CU by LDS, 48, 64 or 96 features each
+// (96: two waves and a rotated k walk), the one whose busiest CU streams the
+// fewest 16-feature tiles, ceil(workgroups / 256) * FT, the widest on a tie
+// (least x per W byte).  GATED (a gate_up pair per workgroup) takes an even
+// FT.
 constexpr int kRingCUs = 256;
 
-RingCfg ring_cfg(int64_t M, int64_t N, int64_t K) {
+RingCfg ring_cfg(int64_t M, int64_t N, int64_t K, bool gated = false) {
     if (M < 1 || M > kSkMaxM || K < 1 || K > kRingMaxK || N < 1 || N > 0x7fffffff) return {0, 0, 0};
-    RingCfg c = N <= 4096 ? RingCfg{1, 4, 4} : (N <= 8192 ? RingCfg{2, 2, 4} : RingCfg{4, 4, 2});
-    if (c.ft == 4 && N % 48 == 0) {
-        auto load = [&](int64_t ft) { return (N / (16 * ft) + kRingCUs - 1) / kRingCUs * ft; };
-        if (N % 64 != 0 || load(3) < load(4)) c = RingCfg{3, 4, 2};
+    RingCfg c{0, 0, 0};
+    if (N > 8192) {
+        int64_t best = 0;
+        for (const RingCfg cand : {RingCfg{6, 2, 2}, RingCfg{4, 4, 2}, RingCfg{3, 4, 2}}) {
+            if (N % (16 * cand.ft) || K % (128 * cand.ks * cand.d) || (gated && cand.ft % 2)) continue;
+            const int64_t load = (N / (16 * cand.ft) + kRingCUs - 1) / kRingCUs * cand.ft;
+            if (!c.ft || load < best) c = cand, best = load;
+        }
+        return c;
     }
+    if (gated) return c;
+    c = N <= 4096 ? RingCfg{1, 4, 4} : RingCfg{2, 2, 4};
     if (N % (16 * c.ft) || K % (128 * c.ks * c.d)) return {0, 0, 0};
     return c;
 }
 
-template <int MT>
+template <int MT, bool GATED>
 void launch_ring_mt(const RingCfg& c, const bf16_t* x, const bf16_t* w, const bf16_t* bias, bf16_t* y, int M, int N,
                     int K, hipStream_t st) {
     const dim3 grid((unsigned)(N / (16 * c.ft))), block(64 * c.ks);
-    if (c.ft == 1)
-        hipLaunchKernelGGL((ring_gemm_kernel<MT, 4, 4, 1, false>), grid, block, 0, st, x, w, bias, y, M, N, K);
-    else if (c.ft == 2)
-        hipLaunchKernelGGL((ring_gemm_kernel<MT, 2, 4, 2, true>), grid, block, 0, st, x, w, bias, y, M, N, K);
+    if (c.ft == 6)
+        hipLaunchKernelGGL((ring_gemm_kernel<MT, 2, 2, 6, true, GATED>), grid, block, 0, st, x, w, bias, y, M, N, K);
+    else if (c.ft == 4)
+        hipLaunchKernelGGL((ring_gemm_kernel<MT, 4, 2, 4, false, GATED>), grid, block, 0, st, x, w, bias, y, M, N, K);
+    else if (GATED)
+        return;  // ring_cfg gives a gated shape an even FT
     else if (c.ft == 3)
-        hipLaunchKernelGGL((ring_gemm_kernel<MT, 4, 2, 3, false>), grid, block, 0, st, x, w, bias, y, M, N, K);
+        hipLaunchKernelGGL((ring_gemm_kernel<MT, 4, 2, 3, false, false>), grid, block, 0, st, x, w, bias, y, M, N, K);
+    else if (c.ft == 2)
+        hipLaunchKernelGGL((ring_gemm_kernel<MT, 2, 4, 2, true, false>), grid, block, 0, st, x, w, bias, y, M, N, K);
     else
-        hipLaunchKernelGGL((ring_gemm_kernel<MT, 4, 2, 4, false>), grid, block, 0, st, x, w, bias, y, M, N, K);
+        hipLaunchKernelGGL((ring_gemm_kernel<MT, 4, 4, 1, false, false>), grid, block, 0, st, x, w, bias, y, M, N, K);
 }
 
+// GATED: w is gate_up [N = 2 inter, K] and y is [M, inter].
+template <bool GATED>
 int launch_ring(const RingCfg& c, const bf16_t* x, const bf16_t* w, const bf16_t* bias, bf16_t* y, int M, int N, int K,
                 hipStream_t st) {
     if (M <= 16)
-        launch_ring_mt<1>(c, x, w, bias, y, M, N, K, st);
+        launch_ring_mt<1, GATED>(c, x, w, bias, y, M, N, K, st);
     else
-        launch_ring_mt<2>(c, x, w, bias, y, M, N, K, st);
+        launch_ring_mt<2, GATED>(c, x, w, bias, y, M, N, K, st);
     return launch_status(hipGetLastError());
 }
 
@@ -490,8 +538,8 @@ class Gemm {
         if (dtype == CRANE_HIP_BF16) {
             const RingCfg rc = ring_cfg(M, N, K);
             if (rc.ft)
-                return launch_ring(rc, (const bf16_t*)x, (const bf16_t*)w, (const bf16_t*)bias, (bf16_t*)y, (int)M,
-                                   (int)N, (int)K, st);
+                return launch_ring<false>(rc, (const bf16_t*)x, (const bf16_t*)w, (const bf16_t*)bias, (bf16_t*)y,
+                                          (int)M, (int)N, (int)K, st);
         }
         if (dtype == CRANE_HIP_BF16 && skinny_fits(M, N, K))
             return launch_skinny((const bf16_t*)x, (const bf16_t*)w, (const bf16_t*)bias, (bf16_t*)y, (int)M, (int)N,
@@ -506,6 +554,15 @@ class Gemm {
         const hipblasStatus_t s = hipblasLtMatmul(handle_, p->desc, &alpha, w, p->a, x, p->b, &beta, y, p->d, y, p->d,
                                                   &p->algo, ws_, ws_bytes_, st);
         return s == HIPBLAS_STATUS_SUCCESS ? CRANE_HIP_OK : CRANE_HIP_E_LAUNCH;
+    }
+
+    // The gated product out = T(silu(g) * u) of [g | u] = x w^T, w = gate_up
+    // [2 inter, K], in one launch (ring_cfg(M, 2 inter, K, true) must take it).
+    int linear_silu_mul(const void* x, const void* w, void* out, int64_t M, int64_t inter, int64_t K, hipStream_t st) {
+        const RingCfg rc = ring_cfg(M, 2 * inter, K, true);
+        if (!rc.ft) return CRANE_HIP_E_INVALID;
+        return launch_ring<true>(rc, (const bf16_t*)x, (const bf16_t*)w, nullptr, (bf16_t*)out, (int)M, (int)(2 * inter),
+                                 (int)K, st);
     }
 
   private:
@@ -596,4 +653,22 @@ extern "C" int crane_gemm_linear(crane_gemm* g, const void* x, const void* w, co
     if (!crane::aligned16(x) || !crane::aligned16(w) || !crane::aligned16(y) || (bias && !crane::aligned16(bias)))
         return CRANE_HIP_E_ALIGN;
     return g->impl.linear(x, w, bias, y, M, N, K, dtype, (hipStream_t)stream);
+}
+
+extern "C" int crane_gemm_silu_mul_supported(int64_t M, int64_t inter, int64_t K, int dtype) {
+    if (dtype != CRANE_HIP_BF16 || inter <= 0 || inter > 0x3fffffffLL) return 0;
+    return crane::ring_cfg(M, 2 * inter, K, true).ft != 0;
+}
+
+extern "C" int crane_gemm_linear_silu_mul(crane_gemm* g, const void* x, const void* w, void* out, int64_t M,
+                                          int64_t inter, int64_t K, int dtype, void* stream) {
+    if (!g) return CRANE_HIP_E_INVALID;
+    if (dtype != CRANE_HIP_F32 && dtype != CRANE_HIP_BF16) return CRANE_HIP_E_DTYPE;
+    if (M < 0 || inter <= 0 || K <= 0 || M > 0x7fffffffLL || inter > 0x3fffffffLL || K > 0x7fffffffLL)
+        return CRANE_HIP_E_INVALID;
+    if (M == 0) return CRANE_HIP_OK;
+    if (!x || !w || !out) return CRANE_HIP_E_INVALID;
+    if (!crane::aligned16(x) || !crane::aligned16(w) || !crane::aligned16(out)) return CRANE_HIP_E_ALIGN;
+    if (!crane_gemm_silu_mul_supported(M, inter, K, dtype)) return CRANE_HIP_E_INVALID;
+    return g->impl.linear_silu_mul(x, w, out, M, inter, K, (hipStream_t)stream);
 }

@@ -217,7 +217,6 @@ __global__ __launch_bounds__(kRowThreads) void rms_norm_row_kernel(T* __restrict
 // Row counts below this take rms_norm_row_kernel (a workgroup per row).
 constexpr int64_t kFewRows = 1024;
 
-__device__ __forceinline__ float silu(float g) { return g / (1.0f + expf(-g)); }
 // grid (ceil(chunks per row / 256), row slots): thread x of workgroup
 // (bx, by) owns chunk 256 bx + x of rows by, by + gridDim.y, ...  A flat
 // chunk index needed a 64-bit division per chunk, which made the kernel

@@ -9,8 +9,9 @@ merged gate_up Mlp::forward (:570-591).
     q   = qk-norm + rope, K/V into the cache        crane_kv_append_qkv
     a   = attention over the cache                  crane_kv_prefill / crane_kv_decode
     x   = residual + o_proj(a); h = post_norm(x)    crane_gemm_linear, crane_hip_add_rms_norm
-    x   = x + down(silu(gate) * up)                 crane_gemm_linear, crane_hip_silu_mul,
-                                                    crane_hip_residual_add
+    x   = x + down(silu(gate) * up)                 crane_gemm_linear_silu_mul (decode batches;
+                                                    else crane_gemm_linear, crane_hip_silu_mul),
+                                                    crane_gemm_linear, crane_hip_residual_add
 
 The layer owns its KV cache (Attention.kv_cache).  S > 1 tokens is a prefill
 chunk; S == 1 a decode step over every sequence's own length."""
@@ -75,6 +76,6 @@ class DecoderLayer:
             attn = self.cache.prefill(q)
         o = ops.linear(attn.view(B * S, -1), w.o)
         h = ops.add_rms_norm(residual, o, w.post_norm, self.eps)
-        act = ops.silu_mul(ops.linear(h, w.gate_up))
+        act = ops.linear_silu_mul(h, w.gate_up)
         ops.residual_add(residual, ops.linear(act, w.down))
         return residual.view(B, S, H)

@@ -138,7 +138,7 @@ class DecoderModel:
             attn = ops.attention_prefill(q, self.k[a], self.v[a], self.lengths, start_bound, self.scale, True)
         o = ops.linear(attn.view(B * S, Hq * D), w.o)
         h2 = ops.add_rms_norm(residual, o, w.post_norm, eps)
-        return ops.linear(ops.silu_mul(ops.linear(h2, w.gate_up)), w.down)
+        return ops.linear(ops.linear_silu_mul(h2, w.gate_up), w.down)
 
     def _run(self, x: torch.Tensor, positions: torch.Tensor, bound: int, start_bound: int) -> torch.Tensor:
         B, S, H = x.shape

@@ -529,6 +529,31 @@ def linear(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor] =
     return y
 
 
+def linear_silu_mul(x: torch.Tensor, gate_up: torch.Tensor) -> torch.Tensor:
+    """Crane's Mlp gate / up projections and fused_silu_mul: x [..., K] with
+    the merged weight gate_up [2 I, K] (gate rows first) -> silu(gate) * up
+    [..., I].  One launch where the library's gated kernel takes the shape
+    (decode batches, crane_gemm_silu_mul_supported), else linear then
+    silu_mul; the roundings are the same either way."""
+    dev = _dev(x, gate_up)
+    K = x.shape[-1]
+    if gate_up.dim() != 2 or gate_up.shape[1] != K or gate_up.shape[0] % 2:
+        raise CraneHipError(_lib.E_INVALID, f"gate_up must be [2 I, {K}]")
+    inter = gate_up.shape[0] // 2
+    M = x.numel() // K
+    dt = _dtype_code(x)
+    if not _lib.lib().crane_gemm_silu_mul_supported(M, inter, K, dt):
+        return silu_mul(linear(x, gate_up), inter)
+    _contig(x, "x")
+    _contig(gate_up, "gate_up")
+    if gate_up.dtype != x.dtype:
+        raise CraneHipError(_lib.E_DTYPE, f"gate_up dtype {gate_up.dtype} != {x.dtype}")
+    out = torch.empty(x.shape[:-1] + (inter,), dtype=x.dtype, device=dev)
+    check(_lib.lib().crane_gemm_linear_silu_mul(_gemm(dev)._h, x.data_ptr(), gate_up.data_ptr(), out.data_ptr(), M,
+                                                inter, K, dt, _stream(dev)), "linear_silu_mul")
+    return out
+
+
 # ---------------------------------------------------------------- sampling
 # Token selection on the logits (include/crane_sampling.h): Crane's gpu_argmax
 # (greedy) and topk_indices (top-k / top-p candidates), batched over rows.

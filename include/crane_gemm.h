@@ -50,6 +50,25 @@ void crane_gemm_destroy(crane_gemm* g);
 int crane_gemm_linear(crane_gemm* g, const void* x, const void* w, const void* bias, void* y, int64_t M, int64_t N,
                       int64_t K, int dtype, void* stream);
 
+/* 1 when crane_gemm_linear_silu_mul takes the shape, else 0: bf16, M <= 32
+ * token rows, K <= 8192, inter > 4096, and inter a multiple of 48 with K a
+ * multiple of 512 or inter a multiple of 32 with K a multiple of 1024 (the
+ * per-wave ring kernel's gated configurations; the Qwen3-8B decode step's
+ * gate_up, inter 12288, K 4096, is one).  For other shapes run
+ * crane_gemm_linear into a [M, 2 inter] buffer and crane_hip_silu_mul
+ * (crane_layer.h). */
+int crane_gemm_silu_mul_supported(int64_t M, int64_t inter, int64_t K, int dtype);
+
+/* out[M, inter] = T(silu(g) * u) where [g | u] = T(x[M, K] W[2 inter, K]^T),
+ * W the merged gate_up weight (gate rows first): Crane's Mlp gate / up
+ * projections followed by fused_silu_mul (qwen3/modeling.rs:573-585), in one
+ * launch.  The roundings are those of crane_gemm_linear (no bias) followed by
+ * crane_hip_silu_mul: each projection rounded to T, then silu(g) * u in f32
+ * rounded once; the projections' f32 summation order is the kernel's own.
+ * CRANE_HIP_E_INVALID for a shape crane_gemm_silu_mul_supported rejects. */
+int crane_gemm_linear_silu_mul(crane_gemm* g, const void* x, const void* w, void* out, int64_t M, int64_t inter,
+                               int64_t K, int dtype, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -75,6 +75,26 @@ def test_gemm_null_context():
     assert _lib.lib().crane_gemm_linear(None, 16, 16, None, 16, 4, 4, 4, 1, None) == _lib.E_INVALID
 
 
+def test_gated_shape_query():
+    """Which shapes the one-launch gate_up + SiLU*mul takes (host logic, no
+    GPU): bf16, at most 32 token rows, K <= 8192, inter > 4096 with inter a
+    multiple of 48 (K of 512) or of 32 (K of 1024)."""
+    from crane_amd import _lib
+    q = _lib.lib().crane_gemm_silu_mul_supported
+    BF16, F32 = 1, 0
+    assert q(32, 12288, 4096, BF16) == 1      # Qwen3-8B decode gate_up
+    assert q(1, 12288, 512, BF16) == 1
+    assert q(3, 4160, 1024, BF16) == 1        # 32-feature pairs
+    assert q(3, 4160, 512, BF16) == 0         # ... which need K % 1024
+    assert q(33, 12288, 4096, BF16) == 0      # more token rows than the kernel takes
+    assert q(0, 12288, 4096, BF16) == 0
+    assert q(32, 4096, 4096, BF16) == 0       # narrow: the two-call path
+    assert q(32, 12288, 4096, F32) == 0
+    assert q(32, 12296, 4096, BF16) == 0      # inter a multiple of neither 48 nor 32
+    assert q(32, 12288, 12288, BF16) == 0     # K past the ring kernel's limit
+    assert _lib.lib().crane_gemm_linear_silu_mul(None, 16, 16, 16, 4, 12288, 4096, BF16, None) == _lib.E_INVALID
+
+
 # ------------------------------------------------------------------ GPU
 
 def _t(x, dtype, dev):
@@ -131,7 +151,8 @@ def test_linear_streaming_parity(gpu, orc, M, N, K, bias):
     (3, 2048, 6144, True),     # 128 workgroups; 12 stages a wave
     (32, 6144, 4096, True),    # qkv_proj at c3: 32 features x 2 waves, rotated k walk (16 stages)
     (17, 8192, 1024, False),   # a partial second token group; 4 stages a wave, rotation over 4
-    (32, 24576, 1024, True),   # gate_up's N: 48 features x 4 waves (512 workgroups, two per CU), 2-slot ring
+    (32, 24576, 1024, True),   # gate_up's N: 96 features x 2 waves (256 workgroups), rotated k walk
+    (32, 24576, 1536, False),  # ... K a multiple of 512, not of 1024: still 96 features (6 stages a wave)
     (32, 16384, 2048, True),   # 64 features x 4 waves (256 workgroups)
     (9, 9072, 1024, False),    # N a multiple of 48, not of 64: 48 features
     (1, 12288, 2048, False),   # one token row, wide (48 features: 256 workgroups)
@@ -139,9 +160,9 @@ def test_linear_streaming_parity(gpu, orc, M, N, K, bias):
 ])
 def test_linear_ring_parity(gpu, orc, M, N, K, bias):
     """bf16 products with M <= 32 token rows, N a multiple of the workgroup's
-    16/32/48 or 64 features (N <= 4096 / <= 8192 / wider) and K <= 8192 a whole
-    number of the per-wave rings (K % 2048 == 0 for the narrowest, 1024 for
-    the others) run the per-wave ring kernel: the decode step's qkv_proj,
+    16/32 or 48/64/96 features (N <= 4096 / <= 8192 / wider) and K <= 8192 a
+    whole number of the per-wave rings (K % 2048 == 0 for the narrowest, 1024
+    or 512 for the others) run the per-wave ring kernel: the decode step's qkv_proj,
     o_proj, gate_up and lm_head.  Same bar as the library path, and a second
     call repeats the bits (the waves' partial products are added in a fixed
     order)."""
@@ -152,6 +173,59 @@ def test_linear_ring_parity(gpu, orc, M, N, K, bias):
     assert_linear_close(got.float().cpu().numpy(), x, w, b, "bf16", orc, f"ring linear {M}x{N}x{K}")
     got2 = ops.linear(_t(x, "bf16", gpu), _t(w, "bf16", gpu), _t(b, "bf16", gpu) if bias else None)
     assert bool((got == got2).all())
+
+
+def _silu_mul_bound(x, w, orc):
+    """The oracle chain of the gated product and a per-element bound for the
+    GPU: each projection lies within the f32 accumulation bound plus one ulp
+    of its rounding; out = silu(g) u moves by at most |u| |silu'(g)| <= 1.1 |u|
+    per unit of g and |silu(g)| per unit of u, plus two ulps (its own rounding
+    and the f32 exp)."""
+    K = x.shape[-1]
+    gu = orc.linear(x, w, None, "bf16", fused=True)
+    acc = (K * 2.0 ** -24) * (np.abs(x.astype(np.float64)) @ np.abs(w.astype(np.float64)).T)
+    dgu = acc + bf16_ulp(gu)
+    inter = w.shape[0] // 2
+    g, u = gu[:, :inter].astype(np.float64), gu[:, inter:].astype(np.float64)
+    silu = g / (1.0 + np.exp(-g))
+    ref = orc.silu_mul(gu, False, "bf16")
+    bound = 1.1 * np.abs(u) * dgu[:, :inter] + np.abs(silu) * dgu[:, inter:] + 2 * bf16_ulp(ref)
+    return ref, bound
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("M,inter,K", [
+    (32, 12288, 4096),  # Qwen3-8B decode: 48 gate + 48 up features a workgroup, 256 workgroups
+    (17, 9216, 1024),   # partial second token group
+    (1, 12288, 512),    # one token row; each wave's two stages fill the ring once
+    (3, 4160, 1024),    # inter a multiple of 32, not 48: 32 + 32 features, one token group
+    (24, 4160, 2048),   # the same with two token groups
+])
+def test_linear_silu_mul_parity(gpu, orc, M, inter, K):
+    """crane_gemm_linear_silu_mul (one launch) against the oracle chain
+    linear -> silu_mul (candle's Mlp at qwen3/modeling.rs:573-585 with Crane's
+    fused_silu_mul): every element within the propagated accumulation bound,
+    at least 98% bit-identical, the mean-relative bar, and a second call
+    repeats the bits.  The two-call GPU path (ops.linear + ops.silu_mul) lies
+    within the same bound."""
+    from crane_amd import _lib, ops
+    from tolerance import errors, BF16_MEAN_REL
+    assert _lib.lib().crane_gemm_silu_mul_supported(M, inter, K, 1) == 1
+    print(f"linear_silu_mul M={M} inter={inter} K={K}", flush=True)
+    x, w, _ = _case(1700 + M + inter // 64 + K, M, 2 * inter, K, "bf16", False)
+    ref, bound = _silu_mul_bound(x, w, orc)
+    xt, wt = _t(x, "bf16", gpu), _t(w, "bf16", gpu)
+    got = ops.linear_silu_mul(xt, wt)
+    g = got.float().cpu().numpy()
+    assert g.shape == (M, inter)
+    d = np.abs(g.astype(np.float64) - ref)
+    assert np.all(d <= bound), f"gated {M}x{inter}x{K}: beyond the bound by {float((d - bound).max())}"
+    exact = float(np.mean(g == ref))
+    assert exact >= 0.98, f"gated {M}x{inter}x{K}: only {exact:.4f} bit-identical"
+    assert errors(g, ref)[1] <= BF16_MEAN_REL
+    assert bool((ops.linear_silu_mul(xt, wt) == got).all())
+    two = ops.silu_mul(ops.linear(xt, wt)).float().cpu().numpy()
+    assert np.all(np.abs(two.astype(np.float64) - ref) <= bound)
 
 
 N_RANDOM = int(os.environ.get("CRANE_RANDOM_GEMM", 12))
