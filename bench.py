@@ -302,8 +302,9 @@ def bench_layer(args, dev, stream, lib):
 def bench_gemm(args, dev, stream, lib):
     """The projections (include/crane_gemm.h): Qwen2.5-7B qkv_proj (with bias)
     and o_proj at config 4's 8 x 4096 rows (hipBLASLt), and at config 3's 32
-    decode rows the Qwen3-8B qkv_proj, o_proj, gate_up and lm_head (the
-    per-wave ring kernel) and down_proj (hipBLASLt).  The decode shapes rotate
+    decode rows the Qwen3-8B qkv_proj, o_proj, gate_up (alone, and with the
+    SiLU*mul in the same launch) and lm_head (the per-wave ring kernel) and
+    down_proj (hipBLASLt).  The decode shapes rotate
     over enough weight copies (> 600 MB) that every launch streams its weight
     from HBM, not from the 256 MB Infinity Cache."""
     import ctypes
@@ -315,24 +316,29 @@ def bench_gemm(args, dev, stream, lib):
     res = {}
     for tag, M, N, K, bias in (("c4_qkv_proj", 8 * 4096, 4608, 3584, True), ("c4_o_proj", 8 * 4096, 3584, 3584, False),
                                ("c3_qkv_proj", 32, 6144, 4096, False), ("c3_o_proj", 32, 4096, 4096, False),
-                               ("c3_gate_up", 32, 24576, 4096, False), ("c3_down_proj", 32, 4096, 12288, False),
-                               ("c3_lm_head", 32, 151936, 4096, False)):
+                               ("c3_gate_up", 32, 24576, 4096, False), ("c3_gate_up_silu_mul", 32, 24576, 4096, False),
+                               ("c3_down_proj", 32, 4096, 12288, False), ("c3_lm_head", 32, 151936, 4096, False)):
         gen = torch.Generator(device=dev).manual_seed(SEED0 + 9)
         x = randn((M, K), gen, torch.bfloat16, dev)
         copies = max(1, -(-600_000_000 // (N * K * 2))) if M <= 64 else 1
         ws_ = [randn((N, K), gen, torch.bfloat16, dev, 1.0 / math.sqrt(K)) for _ in range(copies)]
         b = randn((N,), gen, torch.bfloat16, dev) if bias else None
-        y = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+        gated = tag.endswith("silu_mul")  # one launch: gate_up, then silu(gate) * up [M, N / 2]
+        y = torch.empty((M, N // 2 if gated else N), dtype=torch.bfloat16, device=dev)
 
         def launch(i):
-            rc = lib.crane_gemm_linear(h, x.data_ptr(), ws_[i % copies].data_ptr(),
-                                       b.data_ptr() if b is not None else None, y.data_ptr(), M, N, K, 1, st)
+            if gated:
+                rc = lib.crane_gemm_linear_silu_mul(h, x.data_ptr(), ws_[i % copies].data_ptr(), y.data_ptr(), M,
+                                                    N // 2, K, 1, st)
+            else:
+                rc = lib.crane_gemm_linear(h, x.data_ptr(), ws_[i % copies].data_ptr(),
+                                           b.data_ptr() if b is not None else None, y.data_ptr(), M, N, K, 1, st)
             if rc:
                 raise RuntimeError(f"crane_gemm_linear failed: {rc}")
         ms = timed(launch, args.steps, args.warmup, stream)
         flops = 2.0 * M * N * K
         tf = flops / (ms * 1e-3) / 1e12
-        nbytes = (M * K + N * K + M * N) * 2
+        nbytes = (M * K + N * K + M * (N // 2 if gated else N)) * 2
         res[tag] = dict(us=ms * 1e3, tflops=tf, frac=tf / BF16_PEAK_TFLOPS, gbs=nbytes / (ms * 1e-3) / 1e9)
         log(f"[gemm {tag}] M={M} N={N} K={K}: {ms * 1e3:.1f} us, {tf:.1f} TFLOP/s ({tf / BF16_PEAK_TFLOPS * 100:.1f}% "
             f"of bf16 peak), {res[tag]['gbs']:.0f} GB/s ({res[tag]['gbs'] / HBM_PEAK_GBS * 100:.1f}% of HBM)")
