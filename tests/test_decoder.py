@@ -99,6 +99,9 @@ def _check(got, ref, what):
     ("qwen25_gqa7_bias", 1024, 28, 4, 2048, "rope_only", False, True, 33),
     # Hunyuan order: RoPE, then the norms
     ("hunyuan_order", 512, 8, 2, 1024, "rope_then_norm", True, False, 17),
+    # an intermediate size whose decode step takes the one-launch gate_up + SiLU*mul
+    # (crane_gemm_linear_silu_mul), and o_proj the per-wave ring kernel
+    ("gated_mlp", 1024, 16, 8, 4608, "norm_then_rope", True, False, 24),
 ])
 def test_decoder_layer_prefill_then_decode(gpu, orc, name, hidden, Hq, Hkv, inter, order, qk_norm, bias, S):
     import torch
