@@ -560,7 +560,7 @@ class Gemm {
     // [2 inter, K], in one launch (ring_cfg(M, 2 inter, K, true) must take it).
     int linear_silu_mul(const void* x, const void* w, void* out, int64_t M, int64_t inter, int64_t K, hipStream_t st) {
         const RingCfg rc = ring_cfg(M, 2 * inter, K, true);
-        if (!rc.ft) return CRANE_HIP_E_INVALID;
+        if (rc.ft != 4 && rc.ft != 6) return CRANE_HIP_E_INVALID;  // the gated instantiations
         return launch_ring<true>(rc, (const bf16_t*)x, (const bf16_t*)w, nullptr, (bf16_t*)out, (int)M, (int)(2 * inter),
                                  (int)K, st);
     }
