@@ -223,21 +223,23 @@ int launch_skinny(const bf16_t* x, const bf16_t* w, const bf16_t* bias, bf16_t* 
 // where waves 1.. KS-1 hand their f32 partial products to wave 0 through LDS
 // and wave 0 adds them in wave order (fixed, so a call's bits repeat).
 // Measured at the Qwen3-8B decode shapes (32 rows, weights rotated past the
-// Infinity Cache): o_proj [4096, 4096] 11.2 us against hipBLASLt's 13.9,
-// qkv_proj [6144, 4096] 13.6 against 15.8, gate_up [24576, 4096] 36.7 against
-// the streaming kernel's 43.0, lm_head [151936, 4096] 220 against 238.  The x
+// Infinity Cache): o_proj [4096, 4096] 11.4 us against hipBLASLt's 13.8,
+// qkv_proj [6144, 4096] 13.5 against 15.8, gate_up [24576, 4096] 31.8 against
+// the streaming kernel's 43.0, lm_head [151936, 4096] 221 against 238.  The x
 // reads are what bounds it: without them the same kernel streams W at 5.2-6.0
 // TB/s, and x (the same bytes for every workgroup, read from L2) grows with
 // 32 token rows / 16 FT features per W byte, so wider workgroups pay less x
 // per W byte but leave CUs idle at narrow N.  The configuration follows N:
 //   N <= 4096          FT 1, KS 4, D 4 (at most 256 workgroups)
 //   4096 < N <= 8192   FT 2, KS 2, D 4, each workgroup starting its k walk
-//                      at its own stage (spreads the x reads)
-//   N > 8192           FT 4 or 3, KS 4, D 2: one workgroup per CU (LDS), and
-//                      FT 3 where it evens out the CUs' shares (gate_up:
-//                      512 workgroups of 48 features, 36.7 us, against 384 of
-//                      64, 42.2 us, two rounds either way)
-// down_proj's shape [4096, 12288] stays on hipBLASLt (26.5 us against 29.1).
+//                      at its own stage (spreads the x reads of the two
+//                      waves' halves)
+//   N > 8192           one workgroup per CU (LDS): FT 6 (KS 2, D 2, rotated
+//                      k walk), FT 4 or FT 3 (KS 4, D 2), whichever leaves
+//                      the busiest CU the fewest tiles (gate_up: 256
+//                      workgroups of 96 features 31.8 us, 512 of 48 36.6 us,
+//                      384 of 64 42.2 us)
+// down_proj's shape [4096, 12288] stays on hipBLASLt (26 us against 29).
 
 constexpr int kRingMaxK = 8192;
 
