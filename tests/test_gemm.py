@@ -271,6 +271,38 @@ def test_random_decode_linear(gpu, orc, i):
     assert bool((got == got2).all())
 
 
+def silu_mul_draw(seed: int, i: int):
+    """Draw i of the randomised one-launch gate_up + SiLU*mul sweep: (M, inter,
+    K) that crane_gemm_silu_mul_supported takes -- inter a multiple of 48
+    with K of 512, or of 32 with K of 1024 -- with M * 2 inter * K <= 1.5e9."""
+    r = cases.rng(seed + 9500 + i)
+    M = int(r.integers(1, 33))
+    if i % 2 == 0:
+        inter, K = 48 * int(r.integers(86, 300)), 512 * int(r.integers(1, 9))
+    else:
+        inter, K = 32 * int(r.integers(129, 400)), 1024 * int(r.integers(1, 5))
+    while M * 2 * inter * K > 1.5e9 and K > 1024:
+        K -= 1024
+    return M, inter, K
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("i", range(N_RANDOM // 2))
+def test_random_linear_silu_mul(gpu, orc, i):
+    """Random shapes of the one-launch gated product against the oracle chain,
+    the bar of test_linear_silu_mul_parity."""
+    from crane_amd import _lib, ops
+    M, inter, K = silu_mul_draw(SEED, i)
+    print(f"random linear_silu_mul {i} (seed {SEED}): M={M} inter={inter} K={K}", flush=True)
+    assert _lib.lib().crane_gemm_silu_mul_supported(M, inter, K, 1) == 1
+    x, w, _ = _case(SEED + 9600 + i, M, 2 * inter, K, "bf16", False)
+    ref, bound = _silu_mul_bound(x, w, orc)
+    got = ops.linear_silu_mul(_t(x, "bf16", gpu), _t(w, "bf16", gpu)).float().cpu().numpy()
+    d = np.abs(got.astype(np.float64) - ref)
+    assert np.all(d <= bound), f"random gated {M}x{inter}x{K}: beyond the bound"
+    assert float(np.mean(got == ref)) >= 0.98
+
+
 @pytest.mark.gpu
 def test_qkv_proj_feeds_the_append(gpu, orc):
     """Hidden states -> qkv_proj (bias) -> fused QK-norm/RoPE append, against
