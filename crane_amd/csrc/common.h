@@ -199,6 +199,17 @@ struct PagedRows {
 // Host-side helpers shared by the launchers.
 namespace crane {
 inline int launch_status(hipError_t e) { return e == hipSuccess ? CRANE_HIP_OK : CRANE_HIP_E_LAUNCH; }
+// The device a launch on `stream` runs on: the stream's own device, or the
+// current device for the null stream.  -1 when the runtime cannot tell.
+inline int stream_device(hipStream_t stream) {
+    int dev = -1;
+    if (stream) {
+        if (hipStreamGetDevice(stream, &dev) != hipSuccess) return -1;
+    } else if (hipGetDevice(&dev) != hipSuccess) {
+        return -1;
+    }
+    return dev;
+}
 inline bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 inline int elem_size(int dtype) { return dtype == CRANE_HIP_F32 ? 4 : 2; }
 inline uint32_t f32_bits(float f) { return __builtin_bit_cast(uint32_t, f); }

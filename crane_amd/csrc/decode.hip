@@ -740,16 +740,22 @@ constexpr int kMaxDevices = 64;
 std::mutex scratch_mu;
 void* scratch_ptr[kMaxDevices];  // the array's device address on each GPU, looked up once per device
 
-// The array's address on the current device (set-up on the device's first
-// call: hipGetSymbolAddress with that device current).  Returns a CRANE_HIP_E_*
-// code; *ptr is valid only on success.
-int device_scratch(void** ptr) {
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return CRANE_HIP_E_LAUNCH;
+// The array's address on the device that runs `stream` (set-up on the
+// device's first call: hipGetSymbolAddress with that device current, the
+// caller's current device restored after).  Returns a CRANE_HIP_E_* code;
+// *ptr is valid only on success.
+int device_scratch(hipStream_t stream, void** ptr) {
+    const int dev = stream_device(stream);
+    if (dev < 0 || dev >= kMaxDevices) return CRANE_HIP_E_LAUNCH;
     std::lock_guard<std::mutex> lock(scratch_mu);
     if (!scratch_ptr[dev]) {
+        int cur = -1;
+        if (hipGetDevice(&cur) != hipSuccess) return CRANE_HIP_E_LAUNCH;
+        if (cur != dev && hipSetDevice(dev) != hipSuccess) return CRANE_HIP_E_LAUNCH;
         void* p = nullptr;
-        if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) return CRANE_HIP_E_LAUNCH;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (cur != dev && hipSetDevice(cur) != hipSuccess) return CRANE_HIP_E_LAUNCH;
+        if (e != hipSuccess || !p) return CRANE_HIP_E_LAUNCH;
         scratch_ptr[dev] = p;
     }
     *ptr = scratch_ptr[dev];
@@ -771,7 +777,7 @@ extern "C" int crane_hip_attn_decode_noalloc(const void* q, const void* k_cache,
     if (B == 0) return CRANE_HIP_OK;
     if (ws_layout(B, Hq, n_splits(max_kv), dtype).total > kScratchBytes) return CRANE_HIP_E_WORKSPACE;
     void* ws = nullptr;
-    const int rc = device_scratch(&ws);
+    const int rc = device_scratch((hipStream_t)stream, &ws);
     if (rc) return rc;
     return attn_decode(q, k_cache, v_cache, DenseRows{cache_cap}, kv_len, max_kv, B, Hq, Hkv, D, scale, score_mode, ws,
                        kScratchBytes, out, dtype, stream);
