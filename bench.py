@@ -406,6 +406,9 @@ def bench_sampling(args, dev, stream, lib):
 # ---------------------------------------------------------------- prefill
 
 def bench_prefill(args, dev, stream, lib):
+    """Config 4 causal prefill, once per flags value of --prefill-modes (the
+    first is the headline): 1 = both of candle's score roundings (the
+    library's default), 3 = + CRANE_HIP_PREFILL_LONG_ROWS_ONE_ROUNDING."""
     import torch
     B, S, Hq, Hkv = 8, 4096, 28, 4
     gen = torch.Generator(device=dev).manual_seed(SEED0 + 4)
@@ -416,19 +419,25 @@ def bench_prefill(args, dev, stream, lib):
     start = torch.zeros(B, dtype=torch.int32, device=dev)
     st = stream.cuda_stream
     fn = lib.crane_hip_attn_prefill
-
-    def launch(i):
-        rc = fn(q.data_ptr(), k.data_ptr(), v.data_ptr(), S, start.data_ptr(), 0, B, S, Hq, Hkv, D,
-                1.0 / math.sqrt(D), 1, out.data_ptr(), 1, st)
-        if rc:
-            raise RuntimeError(f"crane_hip_attn_prefill failed: {rc}")
-
-    ms = timed(launch, max(3, args.steps // 2), max(2, args.warmup // 2), stream)
-    pct = launch_percentiles(launch, 100, stream)
     flops = 4.0 * D * Hq * B * S * (S + 1) / 2
-    tflops = flops / (ms * 1e-3) / 1e12
-    log(f"[prefill c4] {ms:.3f} ms/step, {tflops:.1f} TFLOP/s ({tflops / BF16_PEAK_TFLOPS * 100:.1f}% of bf16 peak)")
-    return dict(ms=ms, tflops=tflops, flops=flops, B=B, S=S, Hq=Hq, Hkv=Hkv, pct=pct, _tensors=(q, k, v))
+    modes = [int(x) for x in args.prefill_modes.split(",")]
+    res = {}
+    for flags in modes:
+        def launch(i, flags=flags):
+            rc = fn(q.data_ptr(), k.data_ptr(), v.data_ptr(), S, start.data_ptr(), 0, B, S, Hq, Hkv, D,
+                    1.0 / math.sqrt(D), flags, out.data_ptr(), 1, st)
+            if rc:
+                raise RuntimeError(f"crane_hip_attn_prefill failed: {rc}")
+
+        ms = timed(launch, max(3, args.steps // 2), max(2, args.warmup // 2), stream)
+        pct = launch_percentiles(launch, 100, stream)
+        tflops = flops / (ms * 1e-3) / 1e12
+        log(f"[prefill c4, flags {flags}] {ms:.3f} ms/step, {tflops:.1f} TFLOP/s "
+            f"({tflops / BF16_PEAK_TFLOPS * 100:.1f}% of bf16 peak), median launch {pct[1]:.3f} ms")
+        res[flags] = dict(ms=ms, tflops=tflops, pct=pct)
+    head = res[modes[0]]
+    return dict(ms=head["ms"], tflops=head["tflops"], flops=flops, B=B, S=S, Hq=Hq, Hkv=Hkv, pct=head["pct"],
+                flags=modes[0], modes=res, _tensors=(q, k, v))
 
 
 def bench_prefill_c2(args, dev, stream, lib):
@@ -655,6 +664,10 @@ def main():
     ap.add_argument("--only", choices=["decode", "prefill", "append", "layer", "gemm", "sampling", "model", "all"],
                     default="all")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--prefill-modes", default="1,3",
+                    help="flags values of the timed c4 prefill, the first one the headline: 1 = causal (both of "
+                         "candle's score roundings, the default), 3 = causal + "
+                         "CRANE_HIP_PREFILL_LONG_ROWS_ONE_ROUNDING")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run a plain elementwise kernel over 1 GiB (scales FETCH_SIZE/WRITE_SIZE counters)")
     args = ap.parse_args()
@@ -734,7 +747,12 @@ def main():
                                 "traffic": traffic.get("prefill_c4"), "traffic_source": src,
                                 "kernel": "prefill_bf16_kernel<true>",
                                 "algo_flops_per_launch": pre["flops"]},
-                   "ms_p10_p50_p90": pre["pct"]}
+                   "ms_p10_p50_p90": pre["pct"], "flags": pre["flags"],
+                   "modes": {str(f): {"ms": round(r["ms"], 4), "tflops": round(r["tflops"], 2),
+                                      "frac": round(r["tflops"] / BF16_PEAK_TFLOPS, 4),
+                                      "ms_p10_p50_p90": r["pct"]} for f, r in pre["modes"].items()},
+                   "modes_note": "flags 1: causal, both of candle's score roundings (the library default); "
+                                 "flags 3: + CRANE_HIP_PREFILL_LONG_ROWS_ONE_ROUNDING (opt-in)"}
         if "prefill" in cpu:
             pre_obj["cpu_baseline"] = cpu["prefill"]
         if dec is None:

@@ -266,12 +266,22 @@ def attention_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tens
 
 # --------------------------------------------------------------- prefill op
 
+PREFILL_CAUSAL = 1                  # CRANE_HIP_PREFILL_CAUSAL
+PREFILL_LONG_ROWS_ONE_ROUNDING = 2  # CRANE_HIP_PREFILL_LONG_ROWS_ONE_ROUNDING
+
+
+def _prefill_flags(causal: bool, long_rows_one_rounding: bool) -> int:
+    return (PREFILL_CAUSAL if causal else 0) | (PREFILL_LONG_ROWS_ONE_ROUNDING if long_rows_one_rounding else 0)
+
+
 def attention_prefill(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
                       start_pos: torch.Tensor, max_start: int, scale: Optional[float] = None,
-                      causal: bool = True) -> torch.Tensor:
+                      causal: bool = True, long_rows_one_rounding: bool = False) -> torch.Tensor:
     """Causal GQA prefill: q [B, Hq, S, D] against cache rows [0, start_pos[b]+S).
     Returns [B, S, Hq*D].  Replaces qwen3/modeling.rs:469-502 with the mask of
-    :866-884."""
+    :866-884.  bf16 scores follow both of candle's roundings (:487-488);
+    long_rows_one_rounding=True opts in to the first one only in query tiles
+    whose rows see 1024 keys or more (CRANE_HIP_PREFILL_LONG_ROWS_ONE_ROUNDING)."""
     dev = _dev(q, k_cache, v_cache, start_pos)
     if q.dim() != 4:
         raise CraneHipError(_lib.E_INVALID, "q must be [B, Hq, S, D]")
@@ -290,7 +300,8 @@ def attention_prefill(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Ten
     out = torch.empty((B, S, Hq * D), dtype=q.dtype, device=dev)
     rc = _lib.lib().crane_hip_attn_prefill(
         q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), k_cache.shape[2], start_pos.data_ptr(),
-        max_start, B, S, Hq, k_cache.shape[1], D, scale, int(bool(causal)), out.data_ptr(), dt, _stream(dev))
+        max_start, B, S, Hq, k_cache.shape[1], D, scale, _prefill_flags(causal, long_rows_one_rounding),
+        out.data_ptr(), dt, _stream(dev))
     check(rc, "attention_prefill")
     return out
 
@@ -369,7 +380,8 @@ def attention_decode_paged(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.
 
 def attention_prefill_paged(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tensor,
                             block_table: torch.Tensor, start_pos: torch.Tensor, max_start: int,
-                            scale: Optional[float] = None, causal: bool = True) -> torch.Tensor:
+                            scale: Optional[float] = None, causal: bool = True,
+                            long_rows_one_rounding: bool = False) -> torch.Tensor:
     """attention_prefill over a paged cache: q [B, Hq, S, D]; [B, S, Hq*D]."""
     dev = _dev(q, k_pool, v_pool, block_table, start_pos)
     if q.dim() != 4 or q.shape[3] != HEAD_DIM:
@@ -383,8 +395,8 @@ def attention_prefill_paged(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch
     out = torch.empty((B, S, Hq * D), dtype=q.dtype, device=dev)
     rc = _lib.lib().crane_hip_attn_prefill_paged(
         q.data_ptr(), k_pool.data_ptr(), v_pool.data_ptr(), n_pages, page_rows, block_table.data_ptr(), stride,
-        start_pos.data_ptr(), max_start, B, S, Hq, Hkv, D, scale, int(bool(causal)), out.data_ptr(), dt,
-        _stream(dev))
+        start_pos.data_ptr(), max_start, B, S, Hq, Hkv, D, scale, _prefill_flags(causal, long_rows_one_rounding),
+        out.data_ptr(), dt, _stream(dev))
     check(rc, "attention_prefill_paged")
     return out
 

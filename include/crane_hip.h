@@ -189,6 +189,22 @@ int crane_hip_attn_decode_noalloc(const void* q, const void* k_cache, const void
                                   int dtype, void* stream);
 size_t crane_hip_attn_decode_noalloc_limit(void);
 
+/* Bits of the prefill launchers' `flags` argument.
+ *   CAUSAL  -- key j is visible to query i iff j <= start_pos[b]+i
+ *              (qwen3/modeling.rs:866-884); without it all start_pos[b]+S keys
+ *              are visible.  flags = 0 / 1 keep the meaning of a plain
+ *              causal = false / true.
+ *   LONG_ROWS_ONE_ROUNDING -- opt-in, bf16 only: query tiles of 128 rows whose
+ *              first row sees at least 1024 keys keep candle's first score
+ *              rounding only (q@K^T rounded to T, :487) and fold the scale into
+ *              the exponent, two VALU instructions fewer per score.  The
+ *              second rounding's effect averages out over that many keys, but
+ *              the bits of a row then depend on where its 128-row tile starts.
+ *              Without the flag every score follows both of candle's
+ *              roundings. */
+#define CRANE_HIP_PREFILL_CAUSAL 1
+#define CRANE_HIP_PREFILL_LONG_ROWS_ONE_ROUNDING 2
+
 /* Causal (or full) GQA prefill attention over the cache.
  *
  * q        [B, Hq, S, D] (the prefill q_out of the append)
@@ -196,18 +212,16 @@ size_t crane_hip_attn_decode_noalloc_limit(void);
  * start_pos [B] int32, device: the rows cached before this chunk; query i of
  *          sequence b sits at position start_pos[b]+i
  * max_start host-side bound: start_pos[b] <= max_start and max_start + S <= cache_cap
- * causal   1: key j is visible to query i iff j <= start_pos[b]+i
- *          (qwen3/modeling.rs:866-884); 0: all start_pos[b]+S keys are visible
+ * flags    CRANE_HIP_PREFILL_* bits (above); any other bit is CRANE_HIP_E_INVALID
  * out      [B, S, Hq*D] (qwen3/modeling.rs:497-500)
  * bf16 scores follow candle's two roundings ((q@K^T) rounded to T, then
- * * scale rounded to T, :487-488) in query tiles whose rows see fewer than
- * 1024 keys, and the first rounding only where every row sees 1024 keys or
- * more; rows whose keys all lie in the first 64 get candle's softmax chain in
- * T exactly.
+ * * scale rounded to T, :487-488) unless LONG_ROWS_ONE_ROUNDING is set; rows
+ * whose keys all lie in the first 64 get candle's softmax chain in T exactly,
+ * other rows an online softmax in f32 over bf16 p.
  * Replaces: qwen3/modeling.rs:469-502 (see the file header). */
 int crane_hip_attn_prefill(const void* q, const void* k_cache, const void* v_cache,
                            int64_t cache_cap, const int32_t* start_pos, int64_t max_start,
-                           int B, int S, int Hq, int Hkv, int D, float scale, int causal,
+                           int B, int S, int Hq, int Hkv, int D, float scale, int flags,
                            void* out, int dtype, void* stream);
 
 /* ---- Paged KV cache ------------------------------------------------------
@@ -255,7 +269,7 @@ int crane_hip_attn_decode_paged(const void* q, const void* k_pool, const void* v
 int crane_hip_attn_prefill_paged(const void* q, const void* k_pool, const void* v_pool,
                                  int64_t n_pages, int page_rows, const int32_t* block_table,
                                  int64_t table_stride, const int32_t* start_pos, int64_t max_start,
-                                 int B, int S, int Hq, int Hkv, int D, float scale, int causal,
+                                 int B, int S, int Hq, int Hkv, int D, float scale, int flags,
                                  void* out, int dtype, void* stream);
 
 /* Library and kernel-build identification, e.g. "crane_hip 1 gfx950". */

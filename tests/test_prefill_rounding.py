@@ -6,19 +6,23 @@ candle's prefill SDPA (qwen3/modeling.rs:485-494; hunyuan_dense/modeling.rs
 (:493, candle-nn ops.rs CPU path) e = exp(s - max) (with s - max rounded
 first), the row sum, and p = e / sum, before the f32 P V product (:494).
 
-`kernel_model` restates the committed kernel's arithmetic (prefill.hip) in
-numpy, one wave of 32 query rows and one 64-key tile at a time:
-  - both score roundings (:487-488) for every key;
+`kernel_model` restates the committed kernel's arithmetic (prefill.hip and
+its assembly step, gen_prefill_step.py) in numpy, one wave of 32 query rows
+and one 64-key tile at a time:
+  - both score roundings (:487-488) for every key (the default), or the first
+    only in 128-row tiles whose first row sees LONG_ROW_KEYS keys
+    (CRANE_HIP_PREFILL_LONG_ROWS_ONE_ROUNDING);
   - waves whose rows see keys of tile 0 only run candle's softmax chain
-    exactly (the row max, bf16 e, bf16 sum, bf16 p, O = P V);
+    exactly (the row max, bf16 e, bf16 sum, bf16 p = e / sum, O = P V);
   - other rows: the online softmax in the log2 domain with the kernel's lazy
-    rescale rule (the reference max moves only when some lane's tile sum of p
-    -- 32 keys of a row, the keys k with k % 8 < 4 or >= 4 -- exceeds 256, or
-    a row of the wave has no reference yet, and then to the row's raw max
-    times the bf16 scale times log2(e)); p = bf16(exp2(s log2 e - m)); the
-    row sum adds the bf16 p; O += P V in f32; the keys of a tile split into
-    two halves merged at the end when the grid has at most one workgroup per
-    CU; out = bf16(O / l).
+    rescale rule: p = bf16(exp2(fma(s, fac, -m))) is taken against the
+    reference max m, which moves (for every row of the wave, to the row's max
+    of s * fac, or -inf while the row has seen no key) when a row of the wave
+    has no reference yet, or when some lane's sum of its 32 p (keys k with
+    k % 8 < 4, or >= 4) passes 256 or is not finite; O and l are then scaled
+    and the p taken again.  The row sum adds the bf16 p; O += P V in f32; the
+    keys of a tile split into two halves merged at the end when the grid has
+    at most one workgroup per CU; out = bf16(O / l).
 Only the f32 summation order differs from the GPU's.
 
 The test runs the model on the four draws (seed offset 10000: prefill 7, 28,
@@ -40,7 +44,8 @@ from tolerance import BF16_MAX_ABS, BF16_MEAN_REL
 bf = cases.bf16
 LOG2E = np.float32(1.4426950408889634)
 MASK_RAW = np.float32(-1.0e30)
-PSUM_MAX = np.float32(256.0)
+PSUM_MAX = np.float32(256.0)  # a lane's sum of p above it (or not finite) moves m
+NO_KEY = np.float32(-1e28)    # a row max of s * fac at or below it saw no key
 KBM, KBN = 128, 64          # query rows per workgroup, keys per tile
 CUS = 256                   # MI355X compute units (the key split's threshold)
 TAIL_DRAWS = [7, 28, 70, 102]
@@ -87,10 +92,12 @@ def candle_chain(q, k, v, st, causal, relax=()):
 
 
 @np.errstate(invalid="ignore")  # -inf - -inf where a row has no key yet (selected away)
-def kernel_model(q, k, v, st, causal, second_rounding=True, exact_single_tile=True, long_row_keys=LONG_ROW_KEYS):
+def kernel_model(q, k, v, st, causal, second_rounding=True, exact_single_tile=True, long_row_keys=None):
     """The committed kernel's arithmetic (see the module docstring); the two
-    flags switch off the steps added to follow candle, and long_row_keys=None
-    keeps both score roundings in every row."""
+    flags switch off the steps added to follow candle; long_row_keys=
+    LONG_ROW_KEYS models the opt-in first-rounding-only long rows (None: both
+    score roundings in every row, the kernel's default), decided per query
+    tile of KBM rows."""
     B, Hq, S, D = q.shape
     Hkv = k.shape[1]
     n_rep = Hq // Hkv
@@ -136,8 +143,7 @@ def kernel_model(q, k, v, st, causal, second_rounding=True, exact_single_tile=Tr
                         s2 = np.where(km, -np.inf, s_wg[rows][:, ks]).astype(np.float32)
                         mx = s2.max(1, keepdims=True)
                         e = bf(np.exp2(bf(_f32(s2 - mx)) * LOG2E).astype(np.float32))
-                        inv = np.float32(1.0) / bf(e.sum(1, dtype=np.float32))
-                        p = bf(e * inv[:, None])
+                        p = bf(e / bf(e.sum(1, dtype=np.float32))[:, None])
                         O = _f32(p.astype(np.float64) @ V[ks].astype(np.float64))
                         out[b, rows, h] = bf(O)
                         continue
@@ -158,19 +164,25 @@ def kernel_model(q, k, v, st, causal, second_rounding=True, exact_single_tile=Tr
                                            s_wg[rows][:, ksafe]).astype(np.float32)
                             raw_t = np.where(km, MASK_RAW, raw[rows][:, ksafe]).astype(np.float32)
 
-                            def tile_p(m):
-                                neg = np.where(m == -np.inf, np.float32(0), -m).astype(np.float32)
-                                return bf(np.exp2(_f32(s_t * fac + neg[:, None])))
-                            p = tile_p(m_run)
-                            psum = np.stack([p[:, ~half_of].sum(1, dtype=np.float32),
-                                             p[:, half_of].sum(1, dtype=np.float32)])
-                            if not np.all(psum <= PSUM_MAX) or np.any(m_run == -np.inf):
-                                tmax = raw_t.max(1)
-                                tmax = np.where(tmax > np.float32(0.5) * MASK_RAW, tmax * scale_log2,
-                                                -np.inf).astype(np.float32)
+                            def tile_p(m):  # the exp2 argument is one fma
+                                neg = np.where(m == -np.inf, 0.0, -m.astype(np.float64))
+                                with np.errstate(over="ignore", invalid="ignore"):
+                                    return bf(np.exp2(_f32(s_t.astype(np.float64) * np.float64(fac) + neg[:, None])))
+
+                            def moves(p):
+                                with np.errstate(invalid="ignore"):
+                                    ps = np.stack([p[:, ~half_of].sum(1, dtype=np.float32),
+                                                   p[:, half_of].sum(1, dtype=np.float32)])
+                                return not np.all(ps <= PSUM_MAX)
+                            first = np.any(m_run == -np.inf)
+                            p = None if first else tile_p(m_run)
+                            if first or moves(p):
+                                tmax = (s_t.max(1) * np.float32(fac)).astype(np.float32)
+                                tmax = np.where(tmax > NO_KEY, tmax, -np.inf).astype(np.float32)
                                 m_new = np.maximum(m_run, tmax)
-                                alpha = np.where(m_new == -np.inf, np.float32(1),
-                                                 np.exp2(_f32(m_run - m_new))).astype(np.float32)
+                                with np.errstate(invalid="ignore"):
+                                    alpha = np.where(m_new == -np.inf, np.float32(1),
+                                                     np.exp2(_f32(m_run - m_new))).astype(np.float32)
                                 l_run *= alpha
                                 O *= alpha[:, None]
                                 m_run = m_new
@@ -287,45 +299,47 @@ def test_model_is_the_kernel(gpu, seed, i):
 
 @pytest.mark.parametrize("seed,first", [(1, LONG_ROW_KEYS), (2, 2048), (3, 3584)])
 def test_long_rows_keep_the_bar_with_one_rounding(orc, seed, first):
-    """Workgroups whose rows see at least LONG_ROW_KEYS keys keep candle's
-    first score rounding (:487) only: the second (:488) costs two VALU
-    instructions per score, and over many keys its effect averages out.  On
-    N(0,1) rows (config 4's distribution, where q.k has a standard deviation
-    of sqrt(128)) that see `first` to first + 511 keys, the long-row
-    arithmetic stays within half the bar of candle's chain, and the
-    mean-relative distance within 0.6 of its bar (the outputs of long rows are
-    small: means over many V rows); the same rows with both roundings are
-    printed beside it."""
+    """With CRANE_HIP_PREFILL_LONG_ROWS_ONE_ROUNDING (an opt-in), workgroups
+    whose rows see at least LONG_ROW_KEYS keys keep candle's first score
+    rounding (:487) only: the second (:488) costs two VALU instructions per
+    score, and over many keys its effect averages out.  On N(0,1) rows (config
+    4's distribution, where q.k has a standard deviation of sqrt(128)) that
+    see `first` to first + 511 keys, the long-row arithmetic stays within half
+    the bar of candle's chain, and the mean-relative distance within 0.6 of
+    its bar (the outputs of long rows are small: means over many V rows); the
+    default arithmetic (both roundings) is printed beside it."""
     S = 512
     start = first - 1
     q, k, v, st = cases.prefill_case(7000 + seed, 1, S, 4, 1, [start])
     ref = orc.attn_prefill(q, k, v, st, cases.scale(), True, "bf16")
-    d_long = np.abs(kernel_model(q, k, v, st, True).astype(np.float64) - ref)
-    d_both = np.abs(kernel_model(q, k, v, st, True, long_row_keys=None).astype(np.float64) - ref)
+    d_long = np.abs(kernel_model(q, k, v, st, True, long_row_keys=LONG_ROW_KEYS).astype(np.float64) - ref)
+    d_both = np.abs(kernel_model(q, k, v, st, True).astype(np.float64) - ref)
     rel = lambda d: d.mean() / np.abs(ref).mean()
     print(f"rows of {first}..{first + S - 1} keys: first rounding only: max |d| {d_long.max():.4f}, mean-rel {rel(d_long):.2e}; "
           f"both roundings: max |d| {d_both.max():.4f}, mean-rel {rel(d_both):.2e}")
     assert d_long.max() <= BF16_MAX_ABS / 2 and rel(d_long) <= 0.6 * BF16_MEAN_REL
+    assert d_both.max() <= BF16_MAX_ABS / 2 and rel(d_both) <= 0.6 * BF16_MEAN_REL
     assert np.any(d_long != d_both)  # the long-row arithmetic is in effect
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("first,causal", [(LONG_ROW_KEYS, True), (LONG_ROW_KEYS + 200, False)])
-def test_model_is_the_kernel_long_rows(gpu, first, causal):
-    """The model's long-row arithmetic (first score rounding only) is the
-    kernel's: on rows that see `first` keys and more, at least 99% of outputs
-    bit-identical, every one within 2^-6."""
+@pytest.mark.parametrize("first,causal,one_rounding", [(LONG_ROW_KEYS, True, True), (LONG_ROW_KEYS + 200, False, True),
+                                                       (LONG_ROW_KEYS, True, False)])
+def test_model_is_the_kernel_long_rows(gpu, first, causal, one_rounding):
+    """The model's long-row arithmetic is the kernel's, with the opt-in first
+    rounding only and with the default two: on rows that see `first` keys and
+    more, at least 99% of outputs bit-identical, every one within 2^-6."""
     import torch
     from crane_amd import ops
     S = 384
     q, k, v, st = cases.prefill_case(7100 + first, 2, S, 6, 2, [first - 1, first + 63])
-    print(f"model vs kernel, long rows from {first} keys, causal={causal}", flush=True)
+    print(f"model vs kernel, long rows from {first} keys, causal={causal}, one rounding={one_rounding}", flush=True)
     t = lambda x: torch.from_numpy(np.ascontiguousarray(x)).to(torch.bfloat16).to(gpu)
     out = ops.attention_prefill(t(q), t(k), t(v), torch.as_tensor(st, device=gpu), int(st.max()), cases.scale(),
-                                causal)
+                                causal, long_rows_one_rounding=one_rounding)
     torch.cuda.synchronize()
     got = out.float().cpu().numpy()
-    model = kernel_model(q, k, v, st, causal)
+    model = kernel_model(q, k, v, st, causal, long_row_keys=LONG_ROW_KEYS if one_rounding else None)
     same = float(np.mean(got == model))
     d = np.abs(got.astype(np.float64) - model)
     print(f"  bit-identical {same:.5f}, max |d| {d.max():.5f}", flush=True)
