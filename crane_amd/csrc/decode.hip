@@ -42,11 +42,15 @@
 // standard SDPA (qwen3/modeling.rs:485-488 for n_rep == 1, every qwen2.rs
 // decode :196-197) rounds q@K^T to T, then multiplies by the T scale and
 // rounds again.  Either way every rounding point of the scores is reproduced.
-// A sequence that fits one chunk also gets candle's softmax_last_dim chain in
-// T (candle-nn ops.rs, CPU softmax: e = T(exp(T(s - max))), sum in f32 rounded
-// to T, p = T(e / sum), then p @ V with f32 accumulation): the whole row is in
-// the workgroup, so the exact chain costs nothing measurable.  Longer
-// sequences keep the split-KV form (unnormalised bf16 p per chunk, f32 sums).
+// A sequence of at most kChunkShort (256) keys also gets candle's
+// softmax_last_dim chain in T (candle-nn ops.rs, CPU softmax: e =
+// T(exp(T(s - max))), sum in f32 rounded to T, p = T(e / sum), then p @ V with
+// f32 accumulation): the whole row is in one workgroup, so the exact chain
+// costs nothing measurable.  The choice follows the sequence's own length.
+// Longer sequences keep the split-KV form (unnormalised bf16 p per chunk, f32
+// sums); its last bits depend on the chunk size, 512 keys when the launch's
+// max_kv passes kLongKv, else 256, so a long sequence's output can differ in
+// the last bits between batches with different max_kv.
 #include <mutex>
 #include <type_traits>
 
@@ -230,6 +234,10 @@ __device__ __forceinline__ void decode_item(
     // ---- B: per-head chunk max and sum; probabilities to LDS
     const int n_chunks = (L + CH - 1) / CH;
     const bool single = n_chunks == 1;  // uniform: the whole row is in this workgroup
+    // candle's exact chain for a row of at most kChunkShort keys, whatever the
+    // chunk size: a sequence's arithmetic follows its own length, not the
+    // launch's max_kv
+    const bool exact = L <= kChunkShort;
     for (int h = wave; h < G; h += 4) {
         float sv[CH / 64];
         float m = -INFINITY;
@@ -242,7 +250,7 @@ __device__ __forceinline__ void decode_item(
         }
         m = wave_max(m);
         float l = 0.f;
-        if (single) {
+        if (exact) {
             // candle's softmax_last_dim in T over the whole row
             float e[CH / 64];
 #pragma unroll
@@ -362,8 +370,8 @@ __device__ __forceinline__ void decode_item(
     for (int e = tid; e < G * kHeadDim; e += kThreads) {
         const int h = e / kHeadDim, d = e % kHeadDim;
         const float v = red[0][h][d] + red[1][h][d] + red[2][h][d] + red[3][h][d];
-        if (single)  // the whole sequence fits one chunk: p was normalised, finish here
-            Elem<T>::store(out + ((int64_t)b * Hq + h0 + h) * kHeadDim + d, v);
+        if (single)  // the whole sequence fits one chunk: finish here (exact: p was normalised, l = 1)
+            Elem<T>::store(out + ((int64_t)b * Hq + h0 + h) * kHeadDim + d, exact ? v : v / ml[h][1]);
         else if constexpr (kBf16)  // bf16 partials are stored normalised by the chunk's sum (merge weight w l)
             reinterpret_cast<bf16_t*>(ws_o)[(((int64_t)b * Hq + h0 + h) * nsplit + c) * kHeadDim + d] =
                 f32_to_bf16(v / ml[h][1]);

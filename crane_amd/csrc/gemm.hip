@@ -109,16 +109,18 @@ __device__ __forceinline__ void sk_stage(const uint8_t* cur, uint8_t* nxt, int s
                                          const bool (&isw)[SkStage<MT>::kCopies], int wave, int wrow, int r, int q,
                                          f32x4_v (&acc)[MT]) {
     using St = SkStage<MT>;
-    // this wave's copies of stage st have landed (those of st + 1 may fly)
+    // this wave's copies of stage st have landed (those of st + 1 may fly),
+    // and its LDS reads of stage st - 1 have completed (lgkmcnt 0: the
+    // compiler may have left the last products of stage st - 1, and their
+    // waits, below this point)
     if (st + 1 < nst)
-        __builtin_amdgcn_s_waitcnt(0x0F70 | (St::kCopies & 15) | ((St::kCopies >> 4) << 14));
+        __builtin_amdgcn_s_waitcnt(0x0070 | (St::kCopies & 15) | ((St::kCopies >> 4) << 14));
     else
-        __builtin_amdgcn_s_waitcnt(0x0F70);
+        __builtin_amdgcn_s_waitcnt(0x0070);
     // Every wave's copies of stage st have landed and every wave has finished
-    // reading stage st - 1 (its reads completed before the products that used
-    // them).  A plain barrier: a release fence here would wait for the copies
-    // still in flight (they count as LDS writes); the acquire fence keeps the
-    // reads below it.
+    // reading stage st - 1, so the refill below may overwrite it.  A plain
+    // barrier: a release fence here would wait for the copies still in flight
+    // (they count as LDS writes); the acquire fence keeps the reads below it.
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
     if (st + 2 < nst) sk_issue(nxt, src, vofs, isw, St::kCopies, wave, (st + 2) * kSkStageK * 2);

@@ -257,7 +257,7 @@ extern "C" int crane_kv_decode(const crane_kv* kv, const void* q, int Hq, float 
                                  score_mode, workspace, ws_bytes, out, c.dtype(), stream);
 }
 
-extern "C" int crane_kv_prefill(const crane_kv* kv, const void* q, int Hq, int S, float scale, int causal, void* out,
+extern "C" int crane_kv_prefill(const crane_kv* kv, const void* q, int Hq, int S, float scale, int flags, void* out,
                                 void* stream) {
     if (!kv || S < 0) return CRANE_HIP_E_INVALID;
     KvCache& c = const_cast<crane_kv*>(kv)->impl;  // only the scratch start array is written
@@ -269,7 +269,7 @@ extern "C" int crane_kv_prefill(const crane_kv* kv, const void* q, int Hq, int S
     int rc = c.chunk_starts(S, (hipStream_t)stream, &start);
     if (rc) return rc;
     return crane_hip_attn_prefill(q, c.k(), c.v(), c.cap(), start, c.max_len() - S, c.B(), S, Hq, c.Hkv(), c.D(),
-                                  scale, causal, out, c.dtype(), stream);
+                                  scale, flags, out, c.dtype(), stream);
 }
 
 extern "C" int crane_kv_views(const crane_kv* kv, void** k, void** v, int64_t* cap, const int32_t** dev_len,

@@ -280,7 +280,7 @@ class PagedKv {
                                            Hkv_, D_, scale, score_mode, ws, ws_bytes, out, dtype_, st);
     }
 
-    int prefill(const void* q, int Hq, int S, float scale, int causal, void* out, hipStream_t st) {
+    int prefill(const void* q, int Hq, int S, float scale, int flags, void* out, hipStream_t st) {
         if (S < 0) return CRANE_HIP_E_INVALID;
         if (batch_.empty() || S == 0) return CRANE_HIP_OK;
         for (int id : batch_)
@@ -289,7 +289,7 @@ class PagedKv {
         const int rc = launch_status(hipGetLastError());
         if (rc) return rc;
         return crane_hip_attn_prefill_paged(q, k_pool_, v_pool_, n_pages_, P_, d_table_, max_pps_, d_start_,
-                                            max_len() - S, B(), S, Hq, Hkv_, D_, scale, causal, out, dtype_, st);
+                                            max_len() - S, B(), S, Hq, Hkv_, D_, scale, flags, out, dtype_, st);
     }
 
     int read_seq(int id, void* k, void* v, hipStream_t st) {
@@ -458,9 +458,9 @@ extern "C" int crane_pkv_decode(const crane_pkv* pkv, const void* q, int Hq, flo
                : CRANE_HIP_E_INVALID;
 }
 
-extern "C" int crane_pkv_prefill(crane_pkv* pkv, const void* q, int Hq, int S, float scale, int causal, void* out,
+extern "C" int crane_pkv_prefill(crane_pkv* pkv, const void* q, int Hq, int S, float scale, int flags, void* out,
                                  void* stream) {
-    return pkv ? pkv->impl.prefill(q, Hq, S, scale, causal, out, (hipStream_t)stream) : CRANE_HIP_E_INVALID;
+    return pkv ? pkv->impl.prefill(q, Hq, S, scale, flags, out, (hipStream_t)stream) : CRANE_HIP_E_INVALID;
 }
 
 extern "C" int crane_pkv_read_seq(crane_pkv* pkv, int seq_id, void* k, void* v, void* stream) {

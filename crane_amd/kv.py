@@ -18,7 +18,7 @@ import torch
 
 from . import _lib
 from ._lib import CraneHipError, check
-from .ops import HEAD_DIM, _ORDERS, _dev, _dtype_code, _ptr, _rope_inputs, _stream
+from .ops import HEAD_DIM, _ORDERS, _dev, _dtype_code, _prefill_flags, _ptr, _rope_inputs, _stream
 
 _DT = {torch.float32: _lib.F32, torch.bfloat16: _lib.BF16}
 
@@ -187,14 +187,17 @@ class KvCache:
               "crane_kv_decode")
         return out
 
-    def prefill(self, q: torch.Tensor, scale: Optional[float] = None, causal: bool = True) -> torch.Tensor:
+    def prefill(self, q: torch.Tensor, scale: Optional[float] = None, causal: bool = True,
+                long_rows_one_rounding: bool = False) -> torch.Tensor:
         """Attention of q [B, Hq, S, D] (the last S rows of every sequence) over
-        the cache; [B, S, Hq*D]."""
+        the cache; [B, S, Hq*D].  long_rows_one_rounding as in
+        ops.attention_prefill."""
         _check_q(q, 4, self.batch, self.dtype, self.device)
         B, Hq, S, D = q.shape
         out = torch.empty((B, S, Hq * D), dtype=q.dtype, device=q.device)
         check(_lib.lib().crane_kv_prefill(self._h, q.contiguous().data_ptr(), Hq, S, scale if scale else D ** -0.5,
-                                          int(causal), out.data_ptr(), _stream(q.device)), "crane_kv_prefill")
+                                          _prefill_flags(causal, long_rows_one_rounding), out.data_ptr(),
+                                          _stream(q.device)), "crane_kv_prefill")
         return out
 
 
@@ -354,14 +357,17 @@ class PagedKvCache:
               "crane_pkv_decode")
         return out
 
-    def prefill(self, q: torch.Tensor, scale: Optional[float] = None, causal: bool = True) -> torch.Tensor:
+    def prefill(self, q: torch.Tensor, scale: Optional[float] = None, causal: bool = True,
+                long_rows_one_rounding: bool = False) -> torch.Tensor:
         """Attention of q [B, Hq, S, D] (the last S rows of every batch
-        sequence) over its rows; [B, S, Hq*D]."""
+        sequence) over its rows; [B, S, Hq*D].  long_rows_one_rounding as in
+        ops.attention_prefill."""
         _check_q(q, 4, len(self._batch), self.dtype, self.device)
         B, Hq, S, D = q.shape
         out = torch.empty((B, S, Hq * D), dtype=q.dtype, device=q.device)
         check(_lib.lib().crane_pkv_prefill(self._h, q.contiguous().data_ptr(), Hq, S, scale if scale else D ** -0.5,
-                                           int(causal), out.data_ptr(), _stream(q.device)), "crane_pkv_prefill")
+                                           _prefill_flags(causal, long_rows_one_rounding), out.data_ptr(),
+                                           _stream(q.device)), "crane_pkv_prefill")
         return out
 
     def read_sequence(self, sid: int):

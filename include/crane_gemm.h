@@ -15,11 +15,19 @@
  * epilogue (one rounding of acc + b, where candle rounds the product and then
  * the sum), except bf16 products with few token rows (M <= 32), which
  * hand-written kernels run with the same accumulation and rounding: a per-wave
- * ring kernel when K <= 8192 splits into its pipelines (K a multiple of 2048
- * for N <= 4096, of 1024 above; N a multiple of 16, 32, or 48 or 64 features
- * for N <= 4096, <= 8192 or wider: the decode step's qkv_proj, o_proj, gate_up
- * and lm_head), else a streaming kernel for N >= 16384 (N a multiple of 64, K
- * of 128).  A crane_gemm context holds the hipBLASLt handle,
+ * ring kernel when K <= 8192 splits into its pipelines, by these rules:
+ *   N <= 4096:         N a multiple of 16 and K of 2048;
+ *   4096 < N <= 8192:  N a multiple of 32 and K of 1024;
+ *   N > 8192:          of the configurations of 96 features (K a multiple of
+ *                      512), 64 and 48 features (K of 1024) whose N is a
+ *                      multiple of the feature count, the one that gives the
+ *                      busiest CU the fewest features (the first listed on a
+ *                      tie); gate_up + SiLU (crane_gemm_linear_silu_mul) takes
+ *                      96 or 64 only
+ * (the decode step's qkv_proj, o_proj, gate_up and lm_head), else a streaming
+ * kernel for N >= 16384 (N a multiple of 64, K of 128).  The kernel that runs
+ * a shape fixes the f32 summation order of its products.  A crane_gemm
+ * context holds the hipBLASLt handle,
  * a workspace allocated at creation and the algorithm chosen for each shape
  * (the heuristic query runs once per shape).  Conventions otherwise as in
  * crane_hip.h; crane_gemm_linear does not allocate or synchronise.  Calls on

@@ -163,9 +163,12 @@ size_t crane_hip_attn_decode_workspace(int B, int Hq, int Hkv, int D, int64_t ma
  * workspace device scratch of at least crane_hip_attn_decode_workspace(...) bytes,
  *          16-byte aligned, any contents (partial results of the split-KV pass);
  *          calls that overlap in time must not share a workspace.
- * A sequence of at most 256 keys (512 when max_kv > 12288) gets candle's
- * softmax_last_dim chain in the model dtype; longer ones are split over key
- * chunks whose partial results are merged by their log-sum-exp.
+ * A sequence of at most 256 keys gets candle's softmax_last_dim chain in the
+ * model dtype, whatever the other sequences of the batch; longer ones are
+ * split over key chunks (256 keys, 512 when max_kv > 12288) whose partial
+ * results are merged by their log-sum-exp, so the last bits of a long
+ * sequence's output depend on max_kv (the chunk size fixes the f32
+ * summation order).
  * Replaces: qwen3/modeling.rs:432-467 and :1118-1200 (see the file header). */
 int crane_hip_attn_decode(const void* q, const void* k_cache, const void* v_cache,
                           int64_t cache_cap, const int32_t* kv_len, int64_t max_kv, int B,

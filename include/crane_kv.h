@@ -80,8 +80,9 @@ int crane_kv_decode(const crane_kv* kv, const void* q, int Hq, float scale, int 
                     size_t ws_bytes, void* out, void* stream);
 
 /* Causal or full prefill of the last S rows of every sequence (queries q
- * [B, Hq, S, D]; sequence b's chunk starts at row len[b] - S). */
-int crane_kv_prefill(const crane_kv* kv, const void* q, int Hq, int S, float scale, int causal, void* out,
+ * [B, Hq, S, D]; sequence b's chunk starts at row len[b] - S).  flags: the
+ * CRANE_HIP_PREFILL_* bits of crane_hip_attn_prefill (1 = causal). */
+int crane_kv_prefill(const crane_kv* kv, const void* q, int Hq, int S, float scale, int flags, void* out,
                      void* stream);
 
 /* Device pointers of the K and V buffers (NULL before the first use), the

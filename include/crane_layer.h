@@ -11,7 +11,10 @@
  *       [rows, cols] tensor (input_layernorm, post_attention_layernorm, the
  *       final norm): the fused candle ops::rms_norm, f32 sum of squares,
  *       m = sqrt(sum/cols + eps) rounded to T, y = x / m * w with each op
- *       rounded to T.
+ *       rounded to T.  The sum's f32 order depends on the row count: calls
+ *       of fewer than 1024 rows run a workgroup per row, larger ones a wave
+ *       per row, so a row's m (and then its output) can differ in the last
+ *       bit between such calls.  crane_hip_add_rms_norm likewise.
  *   crane_hip_add_rms_norm   `residual + hidden` followed by the next RmsNorm
  *       (qwen3/modeling.rs:666-669, and the next layer's input_layernorm).
  *       Crane's FusedAddRmsNorm (crane-core/src/fused_ops/cuda_impl.rs:200-258)

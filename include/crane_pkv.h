@@ -81,8 +81,9 @@ int crane_pkv_decode(const crane_pkv* pkv, const void* q, int Hq, float scale, i
                      size_t ws_bytes, void* out, void* stream);
 
 /* Causal or full prefill of the last S rows of every batch sequence (queries
- * q [B, Hq, S, D]; sequence b's chunk starts at row len[b] - S). */
-int crane_pkv_prefill(crane_pkv* pkv, const void* q, int Hq, int S, float scale, int causal, void* out,
+ * q [B, Hq, S, D]; sequence b's chunk starts at row len[b] - S).  flags: the
+ * CRANE_HIP_PREFILL_* bits of crane_hip_attn_prefill (1 = causal). */
+int crane_pkv_prefill(crane_pkv* pkv, const void* q, int Hq, int S, float scale, int flags, void* out,
                       void* stream);
 
 /* Copy a live sequence's len rows into k, v [Hkv, len, D] (contiguous). */

@@ -1,8 +1,8 @@
 """What the split-KV decode's bf16 partials cost, measured on a model of the
 kernel's arithmetic (decode.hip, grouped score form, bf16).
 
-For a sequence longer than one chunk (256 keys; 512 past 12288) the kernel
-does not run candle's one softmax row (qwen3/modeling.rs:440-467: q scaled in
+For a sequence longer than 256 keys (one chunk of 256 keys; of 512 when the
+launch's max_kv passes 12288) the kernel does not run candle's one softmax row (qwen3/modeling.rs:440-467: q scaled in
 T, s = T(q.K^T), e = T(exp(T(s - max))), sum rounded to T, p = T(e / sum),
 p V in f32).  Per chunk c it takes the chunk's max m_c, p = T(exp2(s log2 e -
 m_c log2 e)), l_c = the f32 sum of those p, O_c = sum p V in f32, and stores
@@ -46,11 +46,18 @@ def decode_model(q, k, v, lens, max_kv, partial_bf16=True):
             K = k[b, h // n_rep, :L].astype(np.float64)
             V = v[b, h // n_rep, :L].astype(np.float64)
             s = bf((qg.astype(np.float64) @ K.T).astype(np.float32))
-            if L <= CH:  # one chunk: candle's chain exactly
+            if L <= 256:  # at most kChunkShort keys: candle's chain exactly, whatever the chunk size
                 mx = s.max()
                 e = bf(np.exp(bf(np.float32(s - mx))).astype(np.float32))
                 p = bf(e / bf(np.float32(e.sum(dtype=np.float32))))
                 out[b, h] = bf((p.astype(np.float64) @ V).astype(np.float32))
+                continue
+            if L <= CH:  # one 512-key chunk: the split arithmetic, normalised in place
+                m = np.float32(s.max() * LOG2E)
+                p = bf(np.exp2((s * LOG2E - m).astype(np.float32)).astype(np.float32))
+                lc = np.float32(p.sum(dtype=np.float32))
+                O = (p.astype(np.float64) @ V).astype(np.float32)
+                out[b, h] = bf((O / lc).astype(np.float32))
                 continue
             ms, ls, parts = [], [], []
             for j0 in range(0, L, CH):
@@ -77,9 +84,11 @@ def _case(seed, B, Hq, Hkv, lens):
 
 
 SHAPES = [
-    # B, Hq, Hkv, lengths: config 3's first sequences; a long ragged batch
+    # B, Hq, Hkv, lengths: config 3's first sequences; a long ragged batch; a
+    # batch of 512-key chunks (max_kv past 12288) with sequences of one chunk
     (8, 32, 8, None),
     (3, 16, 2, [700, 2049, 5000]),
+    (3, 8, 2, [200, 300, 12300]),
 ]
 
 

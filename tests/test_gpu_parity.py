@@ -100,6 +100,22 @@ def test_decode_zero_length_and_cap_larger_than_len(gpu, orc):
     assert_close(out[1:], ref, "bf16", "zero-length batch")
 
 
+def test_decode_short_rows_do_not_depend_on_the_batch(gpu, orc):
+    """A sequence of at most 256 keys runs candle's exact chain whatever the
+    launch's max_kv (which picks 512-key chunks past 12288): its output is the
+    same bits alone and beside a 13000-key sequence, within the bar of the oracle."""
+    from crane_amd import ops
+    q, k, v, lens = cases.decode_case(79, 2, 8, 2, [200, 13000], dtype="bf16")
+    qd, kd, vd = dev_t(q, "bf16", gpu), dev_t(k, "bf16", gpu), dev_t(v, "bf16", gpu)
+    both = host(ops.attention_decode(qd, kd, vd, i32(lens, gpu), 13000)).reshape(2, 8 * D)
+    alone = host(ops.attention_decode(qd[:1].contiguous(), kd[:1].contiguous(), vd[:1].contiguous(),
+                                      i32(lens[:1], gpu), 200)).reshape(1, 8 * D)
+    assert np.array_equal(both[0], alone[0])
+    ref = orc.attn_decode(q[:1], k[:1], v[:1], lens[:1], cases.scale(), "bf16", orc.DECODE_GROUPED)
+    note(f"  bit-identical to the oracle {np.mean(alone == ref.reshape(1, 8 * D)):.5f}")
+    assert_close(alone, ref.reshape(1, 8 * D), "bf16", "short row")
+
+
 def test_decode_kv_len_clamped_to_max_kv(gpu, orc):
     """A kv_len above the host's max_kv is clamped, never read past."""
     from crane_amd import ops
