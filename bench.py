@@ -342,6 +342,19 @@ def bench_gemm(args, dev, stream, lib):
         res[tag] = dict(us=ms * 1e3, tflops=tf, frac=tf / BF16_PEAK_TFLOPS, gbs=nbytes / (ms * 1e-3) / 1e9)
         log(f"[gemm {tag}] M={M} N={N} K={K}: {ms * 1e3:.1f} us, {tf:.1f} TFLOP/s ({tf / BF16_PEAK_TFLOPS * 100:.1f}% "
             f"of bf16 peak), {res[tag]['gbs']:.0f} GB/s ({res[tag]['gbs'] / HBM_PEAK_GBS * 100:.1f}% of HBM)")
+        if M > 64:
+            # the same product on constant inputs (every x and w element
+            # 2^-6): the MFMA pipes toggle few bits and the chip holds higher
+            # clocks, so the gap to the N(0, 1) figure is the data-dependent
+            # power limit, not the kernel
+            x.fill_(2.0 ** -6)
+            for t in ws_:
+                t.fill_(2.0 ** -6)
+            msc = timed(launch, args.steps, args.warmup, stream)
+            tfc = flops / (msc * 1e-3) / 1e12
+            res[tag].update(us_const_inputs=msc * 1e3, frac_const_inputs=tfc / BF16_PEAK_TFLOPS)
+            log(f"[gemm {tag}] same product on constant inputs: {msc * 1e3:.1f} us, {tfc:.1f} TFLOP/s "
+                f"({tfc / BF16_PEAK_TFLOPS * 100:.1f}% of bf16 peak)")
         del x, ws_, b, y
     lib.crane_gemm_destroy(h)
     torch.cuda.empty_cache()
@@ -573,6 +586,57 @@ def bench_model_step(args, dev, stream, lib):
     return res
 
 
+def bench_model_prefill(args, dev, stream, lib):
+    """One prefill step of a whole Qwen2.5-7B-shape model at config 4's size:
+    28 layers (hidden 3584, 28 q / 4 kv heads with the QKV bias, intermediate
+    18944, rope only), B=8 sequences of 4096 new tokens into empty caches,
+    then the final norm and the lm_head (vocab 152064) on the last position.
+    The step is the model driver's forward (crane_amd/model.py) with the
+    caches reset before every step.  Random weights of the model's shapes; the
+    roofline is MFMA: the flops of every projection (2 M N K) and of the causal
+    attention (4 D Hq per query-key pair) per step."""
+    import torch
+    from crane_amd import decoder, model
+    L, H, Hq, Hkv, I, V = 28, 3584, 28, 4, 18944, 152064
+    B, S = 8, 4096
+    gen = torch.Generator(device=dev).manual_seed(SEED0 + 28)
+    bf = torch.bfloat16
+
+    def w(*shape, std):
+        return randn(shape, gen, bf, dev, std)
+
+    nqkv = (Hq + 2 * Hkv) * D
+    layers = [decoder.LayerWeights(input_norm=torch.ones(H, dtype=bf, device=dev), qkv=w(nqkv, H, std=H ** -0.5),
+                                   o=w(H, Hq * D, std=(Hq * D) ** -0.5),
+                                   post_norm=torch.ones(H, dtype=bf, device=dev), gate_up=w(2 * I, H, std=H ** -0.5),
+                                   down=w(H, I, std=I ** -0.5), qkv_bias=w(nqkv, std=0.1)) for _ in range(L)]
+    cfg = model.ModelConfig(hidden=H, num_heads=Hq, num_kv_heads=Hkv, intermediate=I, num_layers=L, family="qwen2",
+                            max_position=32768)
+    m = model.DecoderModel(cfg, layers, torch.ones(H, dtype=bf, device=dev), w(V, H, std=H ** -0.5), B, S)
+    x = randn((B, S, H), gen, bf, dev)
+    positions = torch.zeros(B, dtype=torch.int32, device=dev)
+
+    def launch(i):
+        m.reset()
+        m.forward(x, positions)
+
+    ms = timed(launch, 3, 1, stream)
+    M = B * S
+    proj = 2.0 * M * H * (nqkv + Hq * D + 2 * I + I) * L  # qkv, o, gate_up, down
+    attn = 4.0 * D * Hq * B * S * (S + 1) / 2 * L
+    head = 2.0 * B * H * V
+    flops = proj + attn + head
+    tflops = flops / (ms * 1e-3) / 1e12
+    log(f"[model prefill] Qwen2.5-7B shape, {L} layers, B={B} x S={S}: {ms:.1f} ms/step, "
+        f"{M / (ms * 1e-3):.0f} tokens/s, {tflops:.1f} TFLOP/s ({tflops / BF16_PEAK_TFLOPS * 100:.1f}% of bf16 peak; "
+        f"projections {proj / flops * 100:.0f}% of the flops, attention {attn / flops * 100:.0f}%)")
+    res = dict(ms=ms, tokens_per_s=M / (ms * 1e-3), tflops=tflops, flops=flops, proj_flops=proj, attn_flops=attn,
+               layers=L)
+    del m, layers, x
+    torch.cuda.empty_cache()
+    return res
+
+
 # ----------------------------------------------------------- CPU baseline
 
 def _timed_runs(fn, min_seconds: float, min_runs: int):
@@ -661,7 +725,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--only", choices=["decode", "prefill", "append", "layer", "gemm", "sampling", "model", "all"],
+    ap.add_argument("--only", choices=["decode", "prefill", "append", "layer", "gemm", "sampling", "model",
+                                       "model_prefill", "all"],
                     default="all")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--prefill-modes", default="1,3",
@@ -714,6 +779,7 @@ def main():
     gem = bench_gemm(args, dev, stream, lib) if args.only in ("gemm", "all") else None
     smp = bench_sampling(args, dev, stream, lib) if args.only in ("sampling", "all") else None
     mod = bench_model_step(args, dev, stream, lib) if args.only in ("model", "all") else None
+    mpf = bench_model_prefill(args, dev, stream, lib) if args.only in ("model_prefill", "all") else None
     cpu = {} if args.no_cpu_baseline else cpu_baseline(dec, pre)
 
     traffic = pmc_traffic()
@@ -795,6 +861,16 @@ def main():
                          "frac": round(mod["gbs"] / HBM_PEAK_GBS, 4),
                          "bytes_per_step": mod["weight_bytes"] + mod["kv_bytes"],
                          "weight_bytes": mod["weight_bytes"], "kv_bytes": mod["kv_bytes"]}}
+    if mpf is not None:
+        line["model_prefill_step"] = {
+            "workload": "Qwen2.5-7B-shape model prefill step (28 layers, QKV bias, final norm, lm_head 152064 on "
+                        "the last position) at c4: B=8 x S=4096 new tokens into empty caches; "
+                        "crane_amd.model.DecoderModel.forward",
+            "ms_per_step": round(mpf["ms"], 3), "tokens_per_s": round(mpf["tokens_per_s"], 1),
+            "roofline": {"bound": "mfma", "achieved": round(mpf["tflops"], 1), "peak": BF16_PEAK_TFLOPS,
+                         "unit": "TFLOP/s", "frac": round(mpf["tflops"] / BF16_PEAK_TFLOPS, 4),
+                         "flops_per_step": mpf["flops"], "projection_flops": mpf["proj_flops"],
+                         "attention_flops": mpf["attn_flops"]}}
     if "decode" in cpu:
         line["cpu_baseline"] = cpu["decode"]
     print(json.dumps(line), flush=True)
