@@ -140,7 +140,8 @@ class DecoderModel:
         h2 = ops.add_rms_norm(residual, o, w.post_norm, eps)
         return ops.linear(ops.linear_silu_mul(h2, w.gate_up), w.down)
 
-    def _run(self, x: torch.Tensor, positions: torch.Tensor, bound: int, start_bound: int) -> torch.Tensor:
+    def _run(self, x: torch.Tensor, positions: torch.Tensor, bound: int, start_bound: int,
+             trace: Optional[list] = None) -> torch.Tensor:
         B, S, H = x.shape
         if B != self.batch or H != self.cfg.hidden or x.dtype != self.dtype:
             raise CraneHipError(E_INVALID, f"x {tuple(x.shape)} {x.dtype} does not match the model")
@@ -155,6 +156,8 @@ class DecoderModel:
         h = ops.rms_norm(residual, self.layers[0].input_norm, eps)
         for i in range(L):
             mlp = self._layer(i, residual, h, positions, lengths_after, S, bound, start_bound)
+            if trace is not None:  # the layer's output is T(residual + mlp), taken by the next add
+                trace.append((residual.clone(), mlp.clone()))
             if i + 1 < L:
                 h = ops.add_rms_norm(residual, mlp, self.layers[i + 1].input_norm, eps)
         self.lengths.add_(S)             # every layer appended S rows per sequence
@@ -165,18 +168,21 @@ class DecoderModel:
             last = ops.rms_norm(x[:, S - 1:, :].contiguous(), self.final_norm, eps)
         return ops.linear(last, self.lm_head) if self.lm_head is not None else last
 
-    def forward(self, x: torch.Tensor, positions: torch.Tensor) -> torch.Tensor:
+    def forward(self, x: torch.Tensor, positions: torch.Tensor, trace: Optional[list] = None) -> torch.Tensor:
         """Qwen3Model::forward over hidden states x [B, S, hidden]: a prefill
         chunk (S > 1, causal over each sequence's cached rows and the chunk) or
         a decode step (S = 1).  positions [B] int32: the rope row of each
         sequence's first new token (forward's start_pos, per sequence).
         Returns the logits of the last position [B, 1, vocab] (the final
-        normed hidden state when there is no lm_head)."""
+        normed hidden state when there is no lm_head).  trace: a list that
+        receives, per layer, copies of the residual stream after the
+        attention half and of the MLP output ([B S, hidden] each; the layer's
+        output is their sum rounded to the model dtype)."""
         S = x.shape[1]
         top = int(self.host_lengths.max()) + S
         if top > self.capacity:
             raise CraneHipError(E_CAPACITY, f"{top} rows > capacity {self.capacity}")
-        out = self._run(x, positions, top if S > 1 else self.capacity, int(self.host_lengths.max()))
+        out = self._run(x, positions, top if S > 1 else self.capacity, int(self.host_lengths.max()), trace)
         self.host_lengths += S
         return out
 
