@@ -32,6 +32,7 @@ import numpy as np
 
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, GB/s
 BF16_PEAK_TFLOPS = 2500.0      # MI355X dense bf16 MFMA, TFLOP/s
+F32_PEAK_TFLOPS = 157.3        # MI355X dense f32 MFMA, TFLOP/s
 METRIC = "decode attn KV GB/s (% of HBM peak) + prefill attn TFLOP/s, Qwen3-8B shape"
 SEED0 = 0xC3A7E000
 D = 128
@@ -505,6 +506,33 @@ def bench_prefill_c2(args, dev, stream, lib):
     return dict(ms=ms, tflops=flops / (ms * 1e-3) / 1e12)
 
 
+def bench_prefill_f32(args, dev, stream, lib):
+    """Config 2's prefill shape (B=1, S=2048, 16 / 8 heads, causal) in f32:
+    the f32 MFMA kernel (v_mfma_f32_32x32x2_f32), against the f32 MFMA peak."""
+    import torch
+    B, S, Hq, Hkv = 1, 2048, 16, 8
+    gen = torch.Generator(device=dev).manual_seed(SEED0 + 21)
+    q = randn((B, Hq, S, D), gen, torch.float32, dev)
+    k = randn((B, Hkv, S, D), gen, torch.float32, dev)
+    v = randn((B, Hkv, S, D), gen, torch.float32, dev)
+    out = torch.empty((B, S, Hq * D), dtype=torch.float32, device=dev)
+    start = torch.zeros(B, dtype=torch.int32, device=dev)
+    st = stream.cuda_stream
+
+    def launch(i):
+        rc = lib.crane_hip_attn_prefill(q.data_ptr(), k.data_ptr(), v.data_ptr(), S, start.data_ptr(), 0, B, S, Hq,
+                                        Hkv, D, 1.0 / math.sqrt(D), 1, out.data_ptr(), 0, st)
+        if rc:
+            raise RuntimeError(f"crane_hip_attn_prefill (f32) failed: {rc}")
+
+    ms = timed(launch, args.steps, args.warmup, stream)
+    flops = 4.0 * D * Hq * B * S * (S + 1) / 2
+    tf = flops / (ms * 1e-3) / 1e12
+    log(f"[prefill c2 f32] {ms * 1e3:.1f} us/step, {tf:.1f} TFLOP/s ({tf / F32_PEAK_TFLOPS * 100:.1f}% of the f32 "
+        f"MFMA peak)")
+    return dict(ms=ms, tflops=tf)
+
+
 def bench_append(args, dev, stream, lib):
     """Fused QK-norm + RoPE + KV append at config 4's prefill size (8 x 4096
     tokens, 28/4 heads, rope only) and config 3's decode step (32 tokens).  At
@@ -782,7 +810,7 @@ def main():
         log("[calibration] 3 x neg over 2^28 f32 (1073741824 B read + 1073741824 B written each)")
         del src, dst
         torch.cuda.empty_cache()
-    dec = pre = c5 = c2 = app = pg = None
+    dec = pre = c5 = c2 = app = pg = pf32 = None
     if args.only in ("decode", "all"):
         dec = bench_decode(args, dev, stream, lib)
         if args.only == "all":
@@ -792,6 +820,7 @@ def main():
         pre = bench_prefill(args, dev, stream, lib)
         if args.only == "all":
             c2 = bench_prefill_c2(args, dev, stream, lib)
+            pf32 = bench_prefill_f32(args, dev, stream, lib)
     if args.only in ("append", "all"):
         app = bench_append(args, dev, stream, lib)
     lay = bench_layer(args, dev, stream, lib) if args.only in ("layer", "all") else None
@@ -856,6 +885,11 @@ def main():
                                    "value": round(pg["gbs"], 2), "unit": "GB/s",
                                    "us_per_step": round(pg["ms"] * 1e3, 2), "frac": round(pg["gbs"] / HBM_PEAK_GBS, 4),
                                    "kernel": "decode_chunk_kernel<PagedRows> + decode_merge_kernel"}
+    if pf32 is not None:
+        line["prefill_c2_f32"] = {"workload": "c2 shape in f32: causal prefill, S=2048, 16/8 heads (f32 MFMA kernel)",
+                                  "us_per_step": round(pf32["ms"] * 1e3, 1), "value": round(pf32["tflops"], 2),
+                                  "unit": "TFLOP/s", "frac": round(pf32["tflops"] / F32_PEAK_TFLOPS, 4),
+                                  "peak": F32_PEAK_TFLOPS}
     if c2 is not None:
         line["prefill_c2"] = {"workload": "c2: Qwen3-0.6B-shape append+causal prefill, S=2048, 16/8 heads",
                               "us_per_step": round(c2["ms"] * 1e3, 2), "tflops": round(c2["tflops"], 2)}

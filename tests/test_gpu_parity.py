@@ -245,6 +245,10 @@ PREFILL_CASES = [
     ("mha_bf16", 1, 300, 4, 4, [0], True, "bf16"),
     ("tiny_S1_bf16", 2, 1, 8, 2, [0, 63], True, "bf16"),
     ("f32_small", 2, 50, 4, 2, [0, 17], True, "f32"),
+    # the f32 MFMA kernel: config 2's shape, continuation chunks over longer caches, non-causal
+    ("c2_shape_f32", 1, 2048, 16, 8, [0], True, "f32"),
+    ("continuation_f32", 2, 300, 8, 2, [0, 700], True, "f32"),
+    ("noncausal_f32", 2, 130, 4, 2, [0, 33], False, "f32"),
 ]
 
 
