@@ -343,7 +343,7 @@ def bench_gemm(args, dev, stream, lib):
         res[tag] = dict(us=ms * 1e3, tflops=tf, frac=tf / BF16_PEAK_TFLOPS, gbs=nbytes / (ms * 1e-3) / 1e9)
         log(f"[gemm {tag}] M={M} N={N} K={K}: {ms * 1e3:.1f} us, {tf:.1f} TFLOP/s ({tf / BF16_PEAK_TFLOPS * 100:.1f}% "
             f"of bf16 peak), {res[tag]['gbs']:.0f} GB/s ({res[tag]['gbs'] / HBM_PEAK_GBS * 100:.1f}% of HBM)")
-        if M > 64:
+        if M > 64 and not args.no_const_inputs:
             # the same product on constant inputs (every x and w element
             # 2^-6): the MFMA pipes toggle few bits and the chip holds higher
             # clocks, so the gap to the N(0, 1) figure is the data-dependent
@@ -449,6 +449,10 @@ def bench_prefill(args, dev, stream, lib):
         log(f"[prefill c4, flags {flags}] {ms:.3f} ms/step, {tflops:.1f} TFLOP/s "
             f"({tflops / BF16_PEAK_TFLOPS * 100:.1f}% of bf16 peak), median launch {pct[1]:.3f} ms")
         res[flags] = dict(ms=ms, tflops=tflops, pct=pct)
+    head = res[modes[0]]
+    if args.no_const_inputs:
+        return dict(ms=head["ms"], tflops=head["tflops"], flops=flops, B=B, S=S, Hq=Hq, Hkv=Hkv, pct=head["pct"],
+                    flags=modes[0], modes=res, ms_const=None, _tensors=(q, k, v))
     # the headline mode on constant inputs (every q, K, V element 2^-6): the
     # same instructions (no tile of the constant rows redoes its softmax
     # either way at this size) with few toggling bits; the gap to the N(0, 1)
@@ -467,8 +471,6 @@ def bench_prefill(args, dev, stream, lib):
     log(f"[prefill c4, flags {flags0}] the same call on constant inputs: {msc:.3f} ms/step, {tfc:.1f} TFLOP/s "
         f"({tfc / BF16_PEAK_TFLOPS * 100:.1f}% of bf16 peak)")
     del qc, kc_, vc_
-    head = res[modes[0]]
-    head["ms_const_inputs"] = msc
     return dict(ms=head["ms"], tflops=head["tflops"], flops=flops, B=B, S=S, Hq=Hq, Hkv=Hkv, pct=head["pct"],
                 flags=modes[0], modes=res, ms_const=msc, _tensors=(q, k, v))
 
@@ -780,6 +782,9 @@ def main():
                     help="flags values of the timed c4 prefill, the first one the headline: 1 = causal (both of "
                          "candle's score roundings, the default), 3 = causal + "
                          "CRANE_HIP_PREFILL_LONG_ROWS_ONE_ROUNDING")
+    ap.add_argument("--no-const-inputs", action="store_true",
+                    help="skip the constant-input legs of the prefill and GEMM benches (for counter runs, so every "
+                         "dispatch of a kernel is the N(0, 1) workload)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run a plain elementwise kernel over 1 GiB (scales FETCH_SIZE/WRITE_SIZE counters)")
     args = ap.parse_args()
@@ -867,8 +872,9 @@ def main():
                                       "ms_p10_p50_p90": r["pct"]} for f, r in pre["modes"].items()},
                    "modes_note": "flags 1: causal, both of candle's score roundings (the library default); "
                                  "flags 3: + CRANE_HIP_PREFILL_LONG_ROWS_ONE_ROUNDING (opt-in)",
-                   "ms_const_inputs": round(pre["ms_const"], 4),
-                   "frac_const_inputs": round(pre["flops"] / (pre["ms_const"] * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4)}
+                   "ms_const_inputs": round(pre["ms_const"], 4) if pre["ms_const"] else None,
+                   "frac_const_inputs": (round(pre["flops"] / (pre["ms_const"] * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4)
+                                         if pre["ms_const"] else None)}
         if "prefill" in cpu:
             pre_obj["cpu_baseline"] = cpu["prefill"]
         if dec is None:
