@@ -357,6 +357,26 @@ def bench_gemm(args, dev, stream, lib):
             log(f"[gemm {tag}] same product on constant inputs: {msc * 1e3:.1f} us, {tfc:.1f} TFLOP/s "
                 f"({tfc / BF16_PEAK_TFLOPS * 100:.1f}% of bf16 peak)")
         del x, ws_, b, y
+    # the decode step's o_proj and down_proj as the model driver runs them: f32
+    # partial products over 4 splits of K (summed by the add + norm that follows)
+    for tag, M, N, K, sp in (("c3_o_proj_split4", 32, 4096, 4096, 4), ("c3_down_proj_split4", 32, 4096, 12288, 4)):
+        gen = torch.Generator(device=dev).manual_seed(SEED0 + 9)
+        x = randn((M, K), gen, torch.bfloat16, dev)
+        copies = max(1, -(-600_000_000 // (N * K * 2)))
+        ws_ = [randn((N, K), gen, torch.bfloat16, dev, 1.0 / math.sqrt(K)) for _ in range(copies)]
+        part = torch.empty((sp, M, N), dtype=torch.float32, device=dev)
+
+        def launch_split(i):
+            rc = lib.crane_gemm_linear_split(h, x.data_ptr(), ws_[i % copies].data_ptr(), part.data_ptr(), M, N, K,
+                                             sp, 1, st)
+            if rc:
+                raise RuntimeError(f"crane_gemm_linear_split failed: {rc}")
+        ms = timed(launch_split, args.steps, args.warmup, stream)
+        nbytes = (M * K + N * K) * 2 + sp * M * N * 4
+        res[tag] = dict(us=ms * 1e3, gbs=nbytes / (ms * 1e-3) / 1e9)
+        log(f"[gemm {tag}] M={M} N={N} K={K}, {sp} f32 partial products: {ms * 1e3:.1f} us, "
+            f"{res[tag]['gbs']:.0f} GB/s ({res[tag]['gbs'] / HBM_PEAK_GBS * 100:.1f}% of HBM)")
+        del x, ws_, part
     lib.crane_gemm_destroy(h)
     torch.cuda.empty_cache()
     return res

@@ -71,6 +71,7 @@ SIGNATURES = {
     # include/crane_layer.h
     "crane_hip_rms_norm": ([_vp, _vp, _vp, _i64, _i, _f, _i, _vp], _i),
     "crane_hip_add_rms_norm": ([_vp, _vp, _vp, _vp, _i64, _i, _f, _i, _vp], _i),
+    "crane_hip_add_rms_norm_parts": ([_vp, _vp, _i, _vp, _vp, _i64, _i, _f, _i, _vp], _i),
     "crane_hip_silu_mul": ([_vp, _vp, _i64, _i, _i, _vp], _i),
     "crane_hip_residual_add": ([_vp, _vp, _i64, _i, _vp], _i),
     # include/crane_sampling.h
@@ -85,6 +86,8 @@ SIGNATURES = {
     "crane_gemm_linear": ([_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i, _vp], _i),
     "crane_gemm_silu_mul_supported": ([_i64, _i64, _i64, _i], _i),
     "crane_gemm_linear_silu_mul": ([_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i, _vp], _i),
+    "crane_gemm_split_supported": ([_i64, _i64, _i64, _i, _i], _i),
+    "crane_gemm_linear_split": ([_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i, _i, _vp], _i),
     # include/crane_pkv.h
     "crane_pkv_create": ([_i, _i, _i, _i, _i64, _i, _i, _vpp], _i),
     "crane_pkv_destroy": ([_vp], None),

@@ -282,10 +282,16 @@ __device__ __forceinline__ void ring_copy(__amdgpu_buffer_rsrc_t src, uint8_t* d
 // T(u)) [M, I]: the workgroup's first FT / 2 tiles are gate rows
 // [8 FT tile, +8 FT), the others the up rows I + 8 FT tile .. of the same
 // features, so each lane holds the gate and up sums of the same outputs.
-template <int MT, int KS, int D, int FT, bool ROT, bool GATED>
+// PARTIAL: K is split over gridDim.y workgroups as well (split ks takes k in
+// [ks K', (ks + 1) K'), K' = K / gridDim.y), and the workgroup writes its f32
+// partial sums, unrounded and without bias, to parts[ks][M][N]; whoever reads
+// the product adds the splits in split order (one rounding of the sum, as the
+// whole product's).  Each workgroup then covers gridDim.y times more features
+// for the same grid, and reads that much less of x per W byte.
+template <int MT, int KS, int D, int FT, bool ROT, bool GATED, bool PARTIAL = false>
 __global__ __launch_bounds__(64 * KS) void ring_gemm_kernel(const bf16_t* __restrict__ x, const bf16_t* __restrict__ w,
                                                             const bf16_t* __restrict__ bias, bf16_t* __restrict__ y,
-                                                            int M, int N, int K) {
+                                                            int M, int N, int K, float* __restrict__ parts) {
     constexpr int kLoads = 4 * FT + 4 * MT;  // loads per stage: W copies, then x fragments
     constexpr int H = GATED ? FT / 2 : FT;   // tiles per W row range
     static_assert(D >= 2 && D <= 4 && FT >= 1 && FT <= 6, "ring depth and width");
@@ -318,7 +324,8 @@ __global__ __launch_bounds__(64 * KS) void ring_gemm_kernel(const bf16_t* __rest
         }
     };
     const int tile = blockIdx.x;
-    const int kw = K / KS, k0 = wave * kw, nst = kw / 128;
+    const int kp = PARTIAL ? K / (int)gridDim.y : K;  // this workgroup's share of K
+    const int kw = kp / KS, k0 = (PARTIAL ? (int)blockIdx.y * kp : 0) + wave * kw, nst = kw / 128;
     const int r = lane & 15, g = lane >> 4;
     // The W resources span the workgroup's rows from this wave's k0: its 16 H
     // rows (GATED: the gate rows, and the up rows N / 2 further).
@@ -400,6 +407,20 @@ __global__ __launch_bounds__(64 * KS) void ring_gemm_kernel(const bf16_t* __rest
 #pragma unroll
                 for (int m = 0; m < MT; ++m) acc[f][m] += part[j][f][m][lane];
     }
+    if (PARTIAL) {
+        float* pp = parts + (int64_t)blockIdx.y * M * N;
+#pragma unroll
+        for (int f = 0; f < FT; ++f) {
+            const int n = (tile * FT + f) * 16 + 4 * g;
+#pragma unroll
+            for (int m = 0; m < MT; ++m) {
+                const int t = 16 * m + r;
+                if (t >= M) continue;
+                *reinterpret_cast<f32x4_v*>(pp + (int64_t)t * N + n) = acc[f][m];
+            }
+        }
+        return;
+    }
     if (GATED) {
         const int I = N / 2;
 #pragma unroll
@@ -473,17 +494,17 @@ void launch_ring_mt(const RingCfg& c, const bf16_t* x, const bf16_t* w, const bf
                     int K, hipStream_t st) {
     const dim3 grid((unsigned)(N / (16 * c.ft))), block(64 * c.ks);
     if (c.ft == 6)
-        hipLaunchKernelGGL((ring_gemm_kernel<MT, 2, 2, 6, true, GATED>), grid, block, 0, st, x, w, bias, y, M, N, K);
+        hipLaunchKernelGGL((ring_gemm_kernel<MT, 2, 2, 6, true, GATED>), grid, block, 0, st, x, w, bias, y, M, N, K, nullptr);
     else if (c.ft == 4)
-        hipLaunchKernelGGL((ring_gemm_kernel<MT, 4, 2, 4, false, GATED>), grid, block, 0, st, x, w, bias, y, M, N, K);
+        hipLaunchKernelGGL((ring_gemm_kernel<MT, 4, 2, 4, false, GATED>), grid, block, 0, st, x, w, bias, y, M, N, K, nullptr);
     else if (GATED)
         return;  // ring_cfg gives a gated shape an even FT
     else if (c.ft == 3)
-        hipLaunchKernelGGL((ring_gemm_kernel<MT, 4, 2, 3, false, false>), grid, block, 0, st, x, w, bias, y, M, N, K);
+        hipLaunchKernelGGL((ring_gemm_kernel<MT, 4, 2, 3, false, false>), grid, block, 0, st, x, w, bias, y, M, N, K, nullptr);
     else if (c.ft == 2)
-        hipLaunchKernelGGL((ring_gemm_kernel<MT, 2, 4, 2, true, false>), grid, block, 0, st, x, w, bias, y, M, N, K);
+        hipLaunchKernelGGL((ring_gemm_kernel<MT, 2, 4, 2, true, false>), grid, block, 0, st, x, w, bias, y, M, N, K, nullptr);
     else
-        hipLaunchKernelGGL((ring_gemm_kernel<MT, 4, 4, 1, false, false>), grid, block, 0, st, x, w, bias, y, M, N, K);
+        hipLaunchKernelGGL((ring_gemm_kernel<MT, 4, 4, 1, false, false>), grid, block, 0, st, x, w, bias, y, M, N, K, nullptr);
 }
 
 // GATED: w is gate_up [N = 2 inter, K] and y is [M, inter].
@@ -495,6 +516,25 @@ int launch_ring(const RingCfg& c, const bf16_t* x, const bf16_t* w, const bf16_t
     else
         launch_ring_mt<2, GATED>(c, x, w, bias, y, M, N, K, st);
     return launch_status(hipGetLastError());
+}
+
+// Split-K partial products (decode rows, M <= 32): 64 features (FT 4) and 4
+// waves per workgroup, K cut into `splits` ranges over gridDim.y, each wave's
+// quarter of its range walked in 128-wide stages through a ring of 2 slots
+// (128 KiB of LDS: one workgroup per CU).  The ring depth, or 0 when the
+// shape does not split this way.
+int split_ring_depth(int64_t M, int64_t N, int64_t K, int64_t splits) {
+    if (M < 1 || M > kSkMaxM || N < 64 || N % 64 || N > 0x7fffffff || splits < 2 || splits > 16) return 0;
+    if (K % (splits * 4 * 256)) return 0;  // whole ring turns: 2 stages of 128 per wave
+    if (K / splits / 4 > kRingMaxK || 16LL * 4 * K * 2 > 0xffffffffLL) return 0;
+    return 2;
+}
+
+template <int MT>
+void launch_split(const bf16_t* x, const bf16_t* w, float* part, int M, int N, int K, int splits, hipStream_t st) {
+    const dim3 grid((unsigned)(N / 64), (unsigned)splits), block(256);
+    hipLaunchKernelGGL((ring_gemm_kernel<MT, 4, 2, 4, false, false, true>), grid, block, 0, st, x, w, nullptr,
+                       nullptr, M, N, K, part);
 }
 
 struct Plan {
@@ -675,4 +715,28 @@ extern "C" int crane_gemm_linear_silu_mul(crane_gemm* g, const void* x, const vo
     if (!crane::aligned16(x) || !crane::aligned16(w) || !crane::aligned16(out)) return CRANE_HIP_E_ALIGN;
     if (!crane_gemm_silu_mul_supported(M, inter, K, dtype)) return CRANE_HIP_E_INVALID;
     return g->impl.linear_silu_mul(x, w, out, M, inter, K, (hipStream_t)stream);
+}
+
+extern "C" int crane_gemm_split_supported(int64_t M, int64_t N, int64_t K, int splits, int dtype) {
+    return dtype == CRANE_HIP_BF16 && crane::split_ring_depth(M, N, K, splits) != 0;
+}
+
+extern "C" int crane_gemm_linear_split(crane_gemm* g, const void* x, const void* w, float* part, int64_t M, int64_t N,
+                                       int64_t K, int splits, int dtype, void* stream) {
+    if (!g) return CRANE_HIP_E_INVALID;
+    if (dtype != CRANE_HIP_F32 && dtype != CRANE_HIP_BF16) return CRANE_HIP_E_DTYPE;
+    if (M < 0 || N <= 0 || K <= 0 || M > 0x7fffffffLL || N > 0x7fffffffLL || K > 0x7fffffffLL)
+        return CRANE_HIP_E_INVALID;
+    if (M == 0) return CRANE_HIP_OK;
+    if (!x || !w || !part) return CRANE_HIP_E_INVALID;
+    if (!crane::aligned16(x) || !crane::aligned16(w) || !crane::aligned16(part)) return CRANE_HIP_E_ALIGN;
+    if (dtype != CRANE_HIP_BF16 || !crane::split_ring_depth(M, N, K, splits)) return CRANE_HIP_E_INVALID;
+    hipStream_t st = (hipStream_t)stream;
+    if (M <= 16)
+        crane::launch_split<1>((const crane::bf16_t*)x, (const crane::bf16_t*)w, part, (int)M, (int)N, (int)K, splits,
+                               st);
+    else
+        crane::launch_split<2>((const crane::bf16_t*)x, (const crane::bf16_t*)w, part, (int)M, (int)N, (int)K, splits,
+                               st);
+    return crane::launch_status(hipGetLastError());
 }

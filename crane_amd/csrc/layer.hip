@@ -214,6 +214,108 @@ __global__ __launch_bounds__(kRowThreads) void rms_norm_row_kernel(T* __restrict
     }
 }
 
+// residual = T(residual + T(sum_s parts[s])), then the norm of the sum, as
+// rms_norm_row_kernel<T, true> with hidden = T(sum_s parts[s]): parts holds
+// the f32 split-K partial sums [n_parts][rows][cols] of the projection whose
+// output is added here (crane_gemm_linear_split), summed in split order and
+// rounded once, as the whole product's output would be.
+template <typename T, int CH>
+__global__ __launch_bounds__(kRowThreads) void add_parts_rms_norm_row_kernel(T* __restrict__ x,
+                                                                             const float* __restrict__ parts,
+                                                                             int n_parts, const T* __restrict__ w,
+                                                                             T* __restrict__ out, int64_t rows,
+                                                                             int cols, float eps) {
+    constexpr int N = Vec<T>::N;
+    __shared__ float part[kRowThreads / 64];
+    const int64_t row = blockIdx.x;
+    const int nch = cols / N;
+    T* xr = x + row * cols;
+    uint4 c[CH], wc[CH];
+    float ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < CH; ++i) {
+        const int idx = i * kRowThreads + (int)threadIdx.x;
+        if (idx < nch) {
+            uint4 a = ld16<true>(xr + idx * N);
+            if (w) wc[i] = ld16<false>(w + idx * N);
+            float va[N], vh[N];
+#pragma unroll
+            for (int e = 0; e < N; ++e) vh[e] = 0.f;
+            for (int sp = 0; sp < n_parts; ++sp) {
+                const float* pp = parts + ((int64_t)sp * rows + row) * cols + (int64_t)idx * N;
+#pragma unroll
+                for (int e = 0; e < N; e += 4) {
+                    const float4 q = *reinterpret_cast<const float4*>(pp + e);
+                    vh[e] += q.x;
+                    vh[e + 1] += q.y;
+                    vh[e + 2] += q.z;
+                    vh[e + 3] += q.w;
+                }
+            }
+            Vec<T>::unpack(a, va);
+#pragma unroll
+            for (int e = 0; e < N; ++e) va[e] += rt<T>(vh[e]);
+            a = Vec<T>::pack(va);
+            st16<true>(xr + idx * N, a);
+            c[i] = a;
+            float v[N];
+            Vec<T>::unpack(a, v);
+#pragma unroll
+            for (int e = 0; e < N; ++e) ss = __builtin_fmaf(v[e], v[e], ss);
+        }
+    }
+    ss = wave_sum(ss);
+    if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = ss;
+    __syncthreads();
+    float total = part[0];
+#pragma unroll
+    for (int v = 1; v < kRowThreads / 64; ++v) total += part[v];
+    const float m = rt<T>(sqrtf(total / (float)cols + eps));
+    const bool fast = m >= 0x1p-60f && m <= 0x1p60f;  // a normal, moderate divisor (div_by); else the division
+    const float rm = 1.0f / m;
+    T* orow = out + row * cols;
+#pragma unroll
+    for (int i = 0; i < CH; ++i) {
+        const int idx = i * kRowThreads + (int)threadIdx.x;
+        if (idx < nch) {
+            float v[N], wv[N];
+            Vec<T>::unpack(c[i], v);
+            if (w) {
+                Vec<T>::unpack(wc[i], wv);
+            } else {
+#pragma unroll
+                for (int e = 0; e < N; ++e) wv[e] = 1.f;
+            }
+            if (fast) {
+#pragma unroll
+                for (int e = 0; e < N; ++e) v[e] = rt<T>(div_by(v[e], m, rm)) * wv[e];
+            } else {
+#pragma unroll
+                for (int e = 0; e < N; ++e) v[e] = rt<T>(v[e] / m) * wv[e];
+            }
+            st16<true>(orow + idx * N, Vec<T>::pack(v));
+        }
+    }
+}
+
+template <typename T>
+int launch_add_parts_norm(T* x, const float* parts, int n_parts, const T* w, T* out, int64_t rows, int cols,
+                          float eps, hipStream_t st) {
+    const int per_thread = (cols / Vec<T>::N + kRowThreads - 1) / kRowThreads;
+#define CRANE_PARTS_CASE(ch)                                                                                      \
+    if (per_thread <= ch) {                                                                                       \
+        hipLaunchKernelGGL((add_parts_rms_norm_row_kernel<T, ch>), dim3((unsigned)rows), dim3(kRowThreads), 0, st, \
+                           x, parts, n_parts, w, out, rows, cols, eps);                                           \
+        return launch_status(hipGetLastError());                                                                  \
+    }
+    CRANE_PARTS_CASE(1)
+    CRANE_PARTS_CASE(2)
+    CRANE_PARTS_CASE(4)
+    CRANE_PARTS_CASE(8)
+#undef CRANE_PARTS_CASE
+    return CRANE_HIP_E_INVALID;
+}
+
 // Row counts below this take rms_norm_row_kernel (a workgroup per row).
 constexpr int64_t kFewRows = 1024;
 
@@ -375,4 +477,19 @@ extern "C" int crane_hip_residual_add(void* residual, const void* hidden, int64_
         hipLaunchKernelGGL(residual_add_kernel<bf16_t>, dim3(stride_grid(n_chunks)), dim3(256), 0, st,
                            (bf16_t*)residual, (const bf16_t*)hidden, n_chunks);
     return launch_status(hipGetLastError());
+}
+
+extern "C" int crane_hip_add_rms_norm_parts(void* residual, const float* parts, int n_parts, const void* w, void* out,
+                                            int64_t rows, int cols, float eps, int dtype, void* stream) {
+    int rc = check_rows(dtype, residual, parts, out, rows, cols);
+    if (rc >= 0) return rc;
+    if (!(eps >= 0.0f) || n_parts < 1 || n_parts > 64 || rows > 0x7fffffffLL) return CRANE_HIP_E_INVALID;
+    if (w && !aligned16(w)) return CRANE_HIP_E_ALIGN;
+    if (out == residual || (const void*)out == (const void*)parts) return CRANE_HIP_E_INVALID;
+    hipStream_t st = (hipStream_t)stream;
+    if (dtype == CRANE_HIP_F32)
+        return launch_add_parts_norm<float>((float*)residual, parts, n_parts, (const float*)w, (float*)out, rows, cols,
+                                            eps, st);
+    return launch_add_parts_norm<bf16_t>((bf16_t*)residual, parts, n_parts, (const bf16_t*)w, (bf16_t*)out, rows,
+                                         cols, eps, st);
 }

@@ -136,9 +136,12 @@ class DecoderModel:
                                         self.workspace, self.score_mode)
         else:
             attn = ops.attention_prefill(q, self.k[a], self.v[a], self.lengths, start_bound, self.scale, True)
-        o = ops.linear(attn.view(B * S, Hq * D), w.o)
+        # In a decode step o_proj and down_proj feed only the adds: their split-K
+        # partial products go straight into add_rms_norm (ops.linear_for_residual).
+        proj = ops.linear_for_residual if S == 1 else ops.linear
+        o = proj(attn.view(B * S, Hq * D), w.o)
         h2 = ops.add_rms_norm(residual, o, w.post_norm, eps)
-        return ops.linear(ops.linear_silu_mul(h2, w.gate_up), w.down)
+        return proj(ops.linear_silu_mul(h2, w.gate_up), w.down)
 
     def _run(self, x: torch.Tensor, positions: torch.Tensor, bound: int, start_bound: int,
              trace: Optional[list] = None) -> torch.Tensor:
@@ -157,7 +160,8 @@ class DecoderModel:
         for i in range(L):
             mlp = self._layer(i, residual, h, positions, lengths_after, S, bound, start_bound)
             if trace is not None:  # the layer's output is T(residual + mlp), taken by the next add
-                trace.append((residual.clone(), mlp.clone()))
+                trace.append((residual.clone(),
+                              mlp.parts.clone() if isinstance(mlp, ops.PartialProduct) else mlp.clone()))
             if i + 1 < L:
                 h = ops.add_rms_norm(residual, mlp, self.layers[i + 1].input_norm, eps)
         self.lengths.add_(S)             # every layer appended S rows per sequence
@@ -177,7 +181,10 @@ class DecoderModel:
         normed hidden state when there is no lm_head).  trace: a list that
         receives, per layer, copies of the residual stream after the
         attention half and of the MLP output ([B S, hidden] each; the layer's
-        output is their sum rounded to the model dtype)."""
+        output is their sum rounded to the model dtype), or, when down_proj
+        ran split (a decode step), its f32 partial products [splits, B S,
+        hidden], whose sum in split order rounded to the dtype is the MLP
+        output."""
         S = x.shape[1]
         top = int(self.host_lengths.max()) + S
         if top > self.capacity:

@@ -427,10 +427,14 @@ def rms_norm(x: torch.Tensor, weight: Optional[torch.Tensor] = None, eps: float 
     return out
 
 
-def add_rms_norm(residual: torch.Tensor, hidden: torch.Tensor, weight: Optional[torch.Tensor] = None,
+def add_rms_norm(residual: torch.Tensor, hidden, weight: Optional[torch.Tensor] = None,
                  eps: float = 1e-6) -> torch.Tensor:
     """residual += hidden (in place, rounded to the dtype), then RmsNorm of the
-    new residual (Crane's FusedAddRmsNorm::fwd).  Returns the normed rows."""
+    new residual (Crane's FusedAddRmsNorm::fwd).  Returns the normed rows.
+    hidden may be a PartialProduct (linear_for_residual): its splits are
+    summed and rounded to the dtype in the same launch."""
+    if isinstance(hidden, PartialProduct):
+        return _add_rms_norm_parts(residual, hidden, weight, eps)
     dev = _dev(residual, hidden, weight)
     if residual.shape != hidden.shape or residual.dtype != hidden.dtype:
         raise CraneHipError(_lib.E_INVALID, "residual and hidden must have the same shape and dtype")
@@ -516,6 +520,62 @@ def release_stream(device: Optional[torch.device] = None, stream: Optional[torch
     key = (dev, st.cuda_stream)
     _WORKSPACES.pop(key, None)
     _GEMMS.pop(key, None)
+
+
+class PartialProduct:
+    """The f32 split-K partial products [splits, M, N] of a projection
+    (crane_gemm_linear_split) whose output only feeds add_rms_norm, which sums
+    them in split order and rounds once, as the whole product's output."""
+
+    def __init__(self, parts: torch.Tensor, dtype: torch.dtype):
+        self.parts, self.dtype = parts, dtype
+
+    @property
+    def shape(self):
+        return self.parts.shape[1:]
+
+
+_SPLITS = (4, 2)  # split counts tried, in order (4: o_proj and down_proj of a decode step)
+
+
+def linear_for_residual(x: torch.Tensor, weight: torch.Tensor):
+    """The projection x [M, K] W^T of a decode step whose output goes only into
+    add_rms_norm (o_proj, down_proj): a PartialProduct when a split of K
+    applies (bf16, M <= 32; crane_gemm_split_supported), else linear(x, weight).
+    The split kernels read x fewer times per weight byte."""
+    dev = _dev(x, weight)
+    K = x.shape[-1]
+    M = x.numel() // K
+    if x.dtype == torch.bfloat16 and weight.dim() == 2 and weight.shape[1] == K and weight.dtype == x.dtype:
+        N = weight.shape[0]
+        for sp in _SPLITS:
+            if _lib.lib().crane_gemm_split_supported(M, N, K, sp, _lib.BF16):
+                _contig(x, "x")
+                _contig(weight, "weight")
+                parts = torch.empty((sp, M, N), dtype=torch.float32, device=dev)
+                check(_lib.lib().crane_gemm_linear_split(_gemm(dev)._h, x.data_ptr(), weight.data_ptr(),
+                                                         parts.data_ptr(), M, N, K, sp, _lib.BF16, _stream(dev)),
+                      "linear_split")
+                return PartialProduct(parts, x.dtype)
+    return linear(x, weight)
+
+
+def _add_rms_norm_parts(residual: torch.Tensor, hidden: PartialProduct, weight: Optional[torch.Tensor],
+                        eps: float) -> torch.Tensor:
+    dev = _dev(residual, hidden.parts, weight)
+    rows, cols = _rows_of(residual, "residual")
+    sp = hidden.parts.shape[0]
+    if hidden.dtype != residual.dtype or tuple(hidden.parts.shape) != (sp, rows, cols):
+        raise CraneHipError(_lib.E_INVALID, "partial products must be [splits, rows, cols] of the residual's dtype")
+    _contig(hidden.parts, "parts")
+    if weight is not None and (weight.dtype != residual.dtype or weight.numel() != cols or
+                               not weight.is_contiguous()):
+        raise CraneHipError(_lib.E_INVALID, "weight must be a contiguous [cols] tensor of the rows' dtype")
+    out = torch.empty_like(residual)
+    check(_lib.lib().crane_hip_add_rms_norm_parts(residual.data_ptr(), hidden.parts.data_ptr(), sp, _ptr(weight),
+                                                  out.data_ptr(), rows, cols, eps, _dtype_code(residual),
+                                                  _stream(dev)), "add_rms_norm")
+    return out
 
 
 def linear(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor] = None) -> torch.Tensor:

@@ -62,6 +62,16 @@ int crane_hip_silu_mul(const void* gate_up, void* out, int64_t rows, int inter, 
 /* residual[i] = T(residual[i] + hidden[i]) for i < n (n a multiple of 8). */
 int crane_hip_residual_add(void* residual, const void* hidden, int64_t n, int dtype, void* stream);
 
+/* crane_hip_add_rms_norm with hidden = T(sum_s parts[s]): parts are the f32
+ * split-K partial products [n_parts, rows, cols] of crane_gemm_linear_split,
+ * summed in split order and rounded once to T (as the whole product's output
+ * would be), then added to residual and normed as there.  Same rounding
+ * points as the projection followed by crane_hip_add_rms_norm (the
+ * projection's f32 summation order aside).  1 <= n_parts <= 64; out may not
+ * alias residual or parts. */
+int crane_hip_add_rms_norm_parts(void* residual, const float* parts, int n_parts, const void* w, void* out,
+                                 int64_t rows, int cols, float eps, int dtype, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -175,6 +175,57 @@ def test_linear_ring_parity(gpu, orc, M, N, K, bias):
     assert bool((got == got2).all())
 
 
+def test_split_shape_query():
+    """Which shapes the split-K partial products take (host logic, no GPU):
+    bf16, at most 32 token rows, N a multiple of 64, K a multiple of 1024 per
+    split with at most 32768 per split, 2 to 16 splits."""
+    from crane_amd import _lib
+    q = _lib.lib().crane_gemm_split_supported
+    BF16, F32 = 1, 0
+    assert q(32, 4096, 4096, 4, BF16) == 1    # Qwen3-8B decode o_proj
+    assert q(32, 4096, 12288, 4, BF16) == 1   # ... and down_proj
+    assert q(1, 64, 2048, 2, BF16) == 1
+    assert q(32, 4096, 4096, 3, BF16) == 0    # K not a multiple of 1024 per split
+    assert q(32, 4096, 2048, 4, BF16) == 0    # 512 per split: less than a ring turn per wave
+    assert q(33, 4096, 4096, 4, BF16) == 0    # more token rows than the kernel takes
+    assert q(32, 4100, 4096, 4, BF16) == 0    # N not a multiple of 64
+    assert q(32, 4096, 4096, 1, BF16) == 0    # no split
+    assert q(32, 4096, 4096, 4, F32) == 0
+    assert q(32, 4096, 65536, 2, BF16) == 1   # 32768 per split: the limit
+    assert q(32, 4096, 131072, 2, BF16) == 0  # ... past it
+    assert _lib.lib().crane_gemm_linear_split(None, 16, 16, 16, 4, 4096, 4096, 4, BF16, None) == _lib.E_INVALID
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("M,N,K,splits", [
+    (32, 4096, 4096, 4),    # o_proj at the c3 decode batch: 64 workgroups x 4 splits
+    (32, 4096, 12288, 4),   # down_proj at c3: 6 stages a wave
+    (5, 1024, 2048, 2),     # one token group; one ring turn a wave
+    (17, 256, 8192, 8),     # a partial second token group, 8 splits
+    (1, 640, 3072, 3),      # one token row, 3 splits
+])
+def test_linear_split_parity(gpu, orc, M, N, K, splits):
+    """The f32 partial products of crane_gemm_linear_split, summed in split
+    order and rounded once, are the product at the library path's bar; a
+    second call repeats the bits."""
+    import torch
+    from crane_amd import _lib, ops
+    print(f"linear split M={M} N={N} K={K} splits={splits}", flush=True)
+    x, w, _ = _case(1700 + M + N // 64 + K, M, N, K, "bf16", False)
+    xd, wd = _t(x, "bf16", gpu), _t(w, "bf16", gpu)
+    outs = []
+    for _ in range(2):
+        parts = torch.empty((splits, M, N), dtype=torch.float32, device=gpu)
+        assert _lib.lib().crane_gemm_linear_split(ops._gemm(gpu)._h, xd.data_ptr(), wd.data_ptr(), parts.data_ptr(),
+                                                  M, N, K, splits, _lib.BF16, ops._stream(gpu)) == 0
+        outs.append(parts.cpu().numpy())
+    assert np.array_equal(outs[0], outs[1])
+    acc = np.zeros((M, N), np.float32)
+    for p in outs[0]:
+        acc = (acc + p).astype(np.float32)
+    assert_linear_close(cases.bf16(acc), x, w, None, "bf16", orc, f"split linear {M}x{N}x{K}/{splits}")
+
+
 def _silu_mul_bound(x, w, orc):
     """The oracle chain of the gated product and a per-element bound for the
     GPU: each projection lies within the f32 accumulation bound plus one ulp

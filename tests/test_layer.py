@@ -151,6 +151,32 @@ def test_rms_norm_parity(gpu, orc, dtype, rows, cols):
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("dtype", ["bf16", "f32"])
+@pytest.mark.parametrize("rows,cols,splits", [(32, 4096, 4), (3, 1024, 2), (1, 8192, 8), (5, 2560, 3)])
+def test_add_rms_norm_parts_parity(gpu, orc, dtype, rows, cols, splits):
+    """add_rms_norm of split-K partial products (ops.PartialProduct): the
+    residual becomes T(residual + T(sum of the splits in split order)), bit
+    for bit, and the norm is the oracle's add + norm of that rounded sum."""
+    import torch
+    from crane_amd import ops
+    print(f"add_rms_norm of {splits} partial products, {dtype} {rows}x{cols}", flush=True)
+    r = _gen(300 + cols, (rows, cols), 3.0, dtype)
+    parts = _gen(301 + cols, (splits, rows, cols), 0.5, "f32")
+    w = cases.cast(_gen(302 + cols, (cols,), 0.3, "f32") + np.float32(1.0), dtype)
+    acc = np.zeros((rows, cols), np.float32)
+    for p in parts:
+        acc = (acc + p).astype(np.float32)
+    h = cases.cast(acc, dtype)
+    rt = _t(r, dtype, gpu)
+    pp = ops.PartialProduct(torch.from_numpy(parts).to(gpu), torch.bfloat16 if dtype == "bf16" else torch.float32)
+    got = _np(ops.add_rms_norm(rt, pp, _t(w, dtype, gpu)))
+    new_r, ref = orc.add_rms_norm(r, h, w, 1e-6, dtype)
+    np.testing.assert_array_equal(_np(rt), new_r)
+    assert_ulp_close(got, ref, dtype, f"add_rms_norm parts {rows}x{cols}", min_exact=0.999)
+    _norm_bar(got, ref, dtype, f"add_rms_norm parts {rows}x{cols}")
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype", ["bf16", "f32"])
 @pytest.mark.parametrize("rows,cols", NORM_SHAPES[:4])
 def test_add_rms_norm_parity(gpu, orc, dtype, rows, cols):
     """The residual is updated bit-exactly (rounded sum), the norm is of that

@@ -211,15 +211,34 @@ def test_decode_graph_replays_match_eager(gpu, orc):
 LAYER_BAR = dict(abs_bar=2e-2, mean_rel_bar=1e-3)
 
 
-@pytest.mark.parametrize("family,L,cla", [("qwen3", 3, 1), ("hunyuan", 4, 2), ("qwen2", 2, 1)])
-def test_stack_layer_by_layer(gpu, orc, family, L, cla):
+def _mlp_of(t):
+    """The MLP output a trace entry records: the bf16 rows, or the f32 split-K
+    partial products summed in split order and rounded once."""
+    x = t.float().cpu().numpy()
+    if x.ndim == 3:
+        acc = np.zeros(x.shape[1:], np.float32)
+        for p in x:
+            acc = (acc + p).astype(np.float32)
+        return cases.bf16(acc)
+    return x
+
+
+@pytest.mark.parametrize("family,L,cla,dims", [("qwen3", 3, 1, None), ("hunyuan", 4, 2, None), ("qwen2", 2, 1, None),
+                                               ("qwen3", 2, 1, (1024, 16, 4, 2048))],
+                         ids=["qwen3", "hunyuan", "qwen2", "qwen3-split-projections"])
+def test_stack_layer_by_layer(gpu, orc, family, L, cla, dims):
     """Each layer of the stack at the one-layer bar: the oracle's layer i runs
     on the GPU's own input to layer i and over the GPU's cache rows of the
     earlier steps, so no earlier layer's error reaches it; then the final norm
     and lm_head on the GPU's last residual.  Prefill, then two decode steps."""
     import torch
-    print(f"decoder stack layer by layer {family}: {L} layers, CLA factor {cla}", flush=True)
-    m, ref = _build(gpu, orc, family, L, cla)
+    print(f"decoder stack layer by layer {family}: {L} layers, CLA factor {cla}, dims {dims}", flush=True)
+    if dims is None:
+        m, ref = _build(gpu, orc, family, L, cla)
+    else:
+        # o_proj K = 2048, down_proj K = 2048: decode steps take the split-K projections
+        hidden, Hq, Hkv, inter = dims
+        m, ref = _build(gpu, orc, family, L, cla, hidden=hidden, Hq=Hq, Hkv=Hkv, inter=inter)
     r = cases.rng(177 + L)
     B, H = m.batch, m.cfg.hidden
     pos = np.array([0, 7], np.int32)
@@ -230,6 +249,8 @@ def test_stack_layer_by_layer(gpu, orc, family, L, cla):
         got = m.forward(torch.from_numpy(x).to(torch.bfloat16).to(gpu), torch.as_tensor(pos, device=gpu), trace)
         torch.cuda.synchronize()
         assert len(trace) == L
+        if dims is not None and S == 1:
+            assert all(t[1].dim() == 3 for t in trace), "the decode step's down_proj ran split"
         res_in = x.reshape(B * S, H)
         for i in range(L):
             # the oracle's cache of the layer's anchor: the GPU's rows of the
@@ -240,7 +261,7 @@ def test_stack_layer_by_layer(gpu, orc, family, L, cla):
             for c_ref, c_gpu in ((ref.kc, m.k), (ref.vc, m.v)):
                 c_ref[a][:, :, :rows] = c_gpu[a][:, :, :rows].float().cpu().numpy()
             want = ref.layer(i, res_in, pos, S)
-            res_mid, mlp = (t.float().cpu().numpy() for t in trace[i])
+            res_mid, mlp = trace[i][0].float().cpu().numpy(), _mlp_of(trace[i][1])
             out = cases.bf16(res_mid + mlp)  # the GPU layer's output: the next add's rounding of the sum
             _check(out, want, 1, f"{family} {step} layer {i} output", **LAYER_BAR)
             res_in = out
