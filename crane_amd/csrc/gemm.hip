@@ -11,7 +11,10 @@
 // W per 2 M flops).  Those whose K is a whole number of the per-wave rings
 // (K <= 8192; the Qwen3-8B decode step's qkv_proj, o_proj, gate_up and
 // lm_head) take the per-wave ring kernel below; other wide ones (N >= 16384)
-// the streaming kernel; the rest, down_proj among them, hipBLASLt.  The
+// the streaming kernel; the rest, down_proj among them, hipBLASLt.  A
+// product whose output only feeds a residual add (a decode step's o_proj and
+// down_proj) can instead leave f32 split-K partial products for the add +
+// norm to sum (crane_gemm_linear_split: the ring kernel's PARTIAL form).  The
 // streaming kernel (measured at the Qwen3-8B decode shapes before the ring
 // kernel: gate_up [24576, 4096] 43 us vs hipBLASLt's 47 us, lm_head
 // [151936, 4096] 241 us vs ~355 us):
@@ -241,7 +244,10 @@ int launch_skinny(const bf16_t* x, const bf16_t* w, const bf16_t* bias, bf16_t* 
 //                      the busiest CU the fewest tiles (gate_up: 256
 //                      workgroups of 96 features 31.8 us, 512 of 48 36.6 us,
 //                      384 of 64 42.2 us)
-// down_proj's shape [4096, 12288] stays on hipBLASLt (26 us against 29).
+// down_proj's shape [4096, 12288] stays on hipBLASLt through
+// crane_gemm_linear (26 us against 29); split over 4 ranges of K with 64
+// features per workgroup (crane_gemm_linear_split) it takes 20.3 us, and
+// o_proj 9.9 us.
 
 constexpr int kRingMaxK = 8192;
 
