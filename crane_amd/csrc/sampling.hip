@@ -316,7 +316,8 @@ __global__ __launch_bounds__(kThreads) void topk_kernel(const float* __restrict_
 //            candidate count;  (2) every workgroup of a row computes t, the
 //            k-th largest of the P slice maxima -- k elements of distinct
 //            slices are >= t, so t is a lower bound of the row's k-th largest
-//            and every answer has a key >= t -- and appends its slice's keys
+//            and every answer has a key >= t (t is taken a little lower
+//            still, to the 16-bit prefix) -- and appends its slice's keys
 //            >= t to the row's candidate list (wave-aggregated atomics);
 //            (3) one workgroup per row ranks the candidates (a few hundred for
 //            real logits; a thread's rank is the count of larger candidates)
@@ -388,18 +389,20 @@ __global__ __launch_bounds__(kSplitThreads) void argmax_part_kernel(const T* __r
 
 __global__ __launch_bounds__(64) void argmax_final_kernel(const uint64_t* __restrict__ part, int P,
                                                           uint32_t* __restrict__ out) {
-    const int row = blockIdx.x;
-    uint64_t best = 0;
-    for (int p = threadIdx.x; p < P; p += 64) {
-        const uint64_t v = part[(int64_t)row * P + p];
-        best = v > best ? v : best;
-    }
+    // P <= kSplitMaxParts: every load is issued before the first compare
+    const uint64_t* pr = part + (int64_t)blockIdx.x * P;
+    uint64_t v[kSplitMaxParts / 64];
+#pragma unroll
+    for (int j = 0; j < kSplitMaxParts / 64; ++j) v[j] = 64 * j + (int)threadIdx.x < P ? pr[64 * j + threadIdx.x] : 0;
+    uint64_t best = v[0];
+#pragma unroll
+    for (int j = 1; j < kSplitMaxParts / 64; ++j) best = v[j] > best ? v[j] : best;
 #pragma unroll
     for (int m = 32; m >= 1; m >>= 1) {
         const uint64_t o = shfl_xor64(best, m);
         best = o > best ? o : best;
     }
-    if (threadIdx.x == 0) out[row] = ~(uint32_t)best;
+    if (threadIdx.x == 0) out[blockIdx.x] = ~(uint32_t)best;
 }
 
 // Per-row block of the top-k workspace: the candidate count, the P slice
@@ -422,14 +425,18 @@ __global__ __launch_bounds__(kSplitThreads) void topk_max_kernel(const float* __
     }
 }
 
-// The k-th largest of the P (<= kSplitMaxParts) keys m[0..P), by one wave:
-// the largest t with at least k keys >= t, bit by bit from the top.
+// A lower bound of the k-th largest of the P (<= kSplitMaxParts) keys
+// m[0..P), by one wave: the largest t with at least k keys >= t, bit by bit
+// over the top 16 bits only (t's low 16 bits are 0).  It lies within the
+// k-th largest key's 16-bit prefix, so it admits at most the few extra keys
+// that share that prefix (none for logits widened from bf16), in half the
+// steps of the exact search.
 __device__ __forceinline__ uint32_t kth_largest_wave(const uint32_t* m, int P, int k, int lane) {
     uint32_t v[kSplitMaxParts / 64];
 #pragma unroll
     for (int j = 0; j < kSplitMaxParts / 64; ++j) v[j] = 64 * j + lane < P ? m[64 * j + lane] : 0u;
     uint32_t t = 0;
-    for (int bit = 31; bit >= 0; --bit) {
+    for (int bit = 31; bit >= 16; --bit) {
         const uint32_t c = t | (1u << bit);
         int cnt = 0;
 #pragma unroll
@@ -485,8 +492,13 @@ __global__ __launch_bounds__(kSplitThreads) void topk_collect_kernel(const float
 __global__ __launch_bounds__(kThreads) void topk_final_kernel(const float* __restrict__ x, int64_t n, int k, int P,
                                                               const uint8_t* __restrict__ ws,
                                                               uint32_t* __restrict__ out) {
+    static_assert(kThreads <= kCand, "one candidate slot per thread");
     const int row = blockIdx.x;
     const uint8_t* rb = ws + (int64_t)row * topk_row_bytes(P);
+    const uint64_t* src = reinterpret_cast<const uint64_t*>(rb + topk_cand_offset(P));
+    // this thread's first slot is loaded beside the count, not after it (the
+    // slots past the count hold stale keys and are dropped)
+    const uint64_t first = src[threadIdx.x];
     const uint32_t count = *reinterpret_cast<const uint32_t*>(rb);
     uint32_t* out_row = out + (int64_t)row * k;
     if (count > (uint32_t)kCand) {  // uniform: long runs of equal values
@@ -494,17 +506,29 @@ __global__ __launch_bounds__(kThreads) void topk_final_kernel(const float* __res
         return;
     }
     __shared__ uint64_t cand[kCand];
-    const uint64_t* src = reinterpret_cast<const uint64_t*>(rb + topk_cand_offset(P));
-    for (uint32_t i = threadIdx.x; i < count; i += kThreads) cand[i] = src[i];
+    // the list padded to a multiple of 8 with 0, which is below every
+    // candidate (the low word ~index is never 0)
+    const uint32_t count8 = (count + 7u) & ~7u;
+    if (threadIdx.x < count) cand[threadIdx.x] = first;
+    else if (threadIdx.x < count8) cand[threadIdx.x] = 0;
+    for (uint32_t i = threadIdx.x + kThreads; i < count; i += kThreads) cand[i] = src[i];
     __syncthreads();
     if (count <= (uint32_t)kThreads) {
         // Up to one candidate per thread: its rank is the number of larger
         // candidates (the keys are distinct: the index is part of them), read
-        // back from LDS as broadcasts; ranks below k are the answer, in order.
-        const uint64_t mine = threadIdx.x < count ? cand[threadIdx.x] : 0;
-        uint32_t rank = 0;
-        for (uint32_t j = 0; j < count; ++j) rank += cand[j] > mine ? 1u : 0u;
-        if (threadIdx.x < count && rank < (uint32_t)k) out_row[rank] = ~(uint32_t)mine;
+        // back from LDS as broadcasts, 8 loads in flight, by the waves that
+        // hold candidates only; ranks below k are the answer, in order.
+        if (threadIdx.x < count) {
+            uint32_t rank = 0;
+            for (uint32_t q = 0; q < count8; q += 8) {
+                uint64_t w[8];
+#pragma unroll
+                for (int e = 0; e < 8; ++e) w[e] = cand[q + e];
+#pragma unroll
+                for (int e = 0; e < 8; ++e) rank += w[e] > first ? 1u : 0u;
+            }
+            if (rank < (uint32_t)k) out_row[rank] = ~(uint32_t)first;
+        }
     } else {
         sort_candidates(cand, count, k, out_row);
     }

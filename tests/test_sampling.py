@@ -148,11 +148,13 @@ def test_split_rows_ties_masks_and_nan(gpu, orc):
     """The split path (few rows of the vocabulary's length, 148 workgroups a
     row) on the tie, mask and NaN rows: equal maxima in different slices, a
     row of equal values (more candidates than the list holds: the exact
-    one-workgroup fallback), fewer finite values than k, NaN runs."""
+    one-workgroup fallback), fewer finite values than k, NaN runs, and slices
+    holding more candidates than their slots (scanned again by the last
+    phase: a hundred such slices, or every slice)."""
     from crane_amd import _lib, ops
     n = VOCAB
-    assert _lib.lib().crane_hip_select_workspace_bytes(8, n) > 0
-    x = cases.bf16(_logits(50, 8, n, std=1.0))
+    assert _lib.lib().crane_hip_select_workspace_bytes(10, n) > 0
+    x = cases.bf16(_logits(50, 10, n, std=1.0))
     x[0, [17, 40000, 151935]] = 9.0               # equal maxima in three slices
     x[1, :] = 2.0                                 # all equal
     x[2, :] = -np.inf
@@ -163,6 +165,9 @@ def test_split_rows_ties_masks_and_nan(gpu, orc):
     x[5, 5] = 8.0
     x[6, :] = np.nan
     x[7, 1000:3000] = 30.0                        # 2000 equal maxima: k of them by index
+    for i in range(100):                          # 10 candidates in each of 100 slices
+        x[8, i * 600 + 7 * np.arange(10)] = 20.0 + (i % 8) / 8
+    x[9, ::100] = 24.0                            # 1520 equal values, 6 in every slice
     print("split rows: argmax", flush=True)
     for dtype in ("bf16", "f32"):
         got = ops.argmax(_t(x, dtype, gpu)).cpu().numpy().astype(np.uint32)
