@@ -156,18 +156,27 @@ __global__ __launch_bounds__(kRowThreads) void rms_norm_row_kernel(T* __restrict
     const int64_t row = blockIdx.x;
     const int nch = cols / N;
     T* xr = x + row * cols;
-    uint4 c[CH], wc[CH];
+    uint4 c[CH], wc[CH], hc[ADD ? CH : 1];
+    // every load of the row is issued before the first store
+#pragma unroll
+    for (int i = 0; i < CH; ++i) {
+        const int idx = i * kRowThreads + (int)threadIdx.x;
+        if (idx < nch) {
+            c[i] = ld16<ADD>(xr + idx * N);
+            if (w) wc[i] = ld16<false>(w + idx * N);
+            if constexpr (ADD) hc[i] = ld16<true>(hidden + row * cols + idx * N);
+        }
+    }
     float ss = 0.f;
 #pragma unroll
     for (int i = 0; i < CH; ++i) {
         const int idx = i * kRowThreads + (int)threadIdx.x;
         if (idx < nch) {
-            uint4 a = ld16<ADD>(xr + idx * N);
-            if (w) wc[i] = ld16<false>(w + idx * N);
+            uint4 a = c[i];
             if constexpr (ADD) {  // residual = T(residual + hidden), stored, and normed as rounded
                 float va[N], vh[N];
                 Vec<T>::unpack(a, va);
-                Vec<T>::unpack(ld16<true>(hidden + row * cols + idx * N), vh);
+                Vec<T>::unpack(hc[i], vh);
 #pragma unroll
                 for (int e = 0; e < N; ++e) va[e] += vh[e];
                 a = Vec<T>::pack(va);
@@ -218,44 +227,72 @@ __global__ __launch_bounds__(kRowThreads) void rms_norm_row_kernel(T* __restrict
 // rms_norm_row_kernel<T, true> with hidden = T(sum_s parts[s]): parts holds
 // the f32 split-K partial sums [n_parts][rows][cols] of the projection whose
 // output is added here (crane_gemm_linear_split), summed in split order and
-// rounded once, as the whole product's output would be.
-template <typename T, int CH>
+// rounded once, as the whole product's output would be.  NP (2 or 4, or 0 for
+// any count) is n_parts known at compile time: then every load of the row --
+// residual, weight and all the partials -- is issued before the first use,
+// one memory round trip in all (with a run-time count each split's loads
+// waited for the previous split's).
+template <typename T, int CH, int NP>
 __global__ __launch_bounds__(kRowThreads) void add_parts_rms_norm_row_kernel(T* __restrict__ x,
                                                                              const float* __restrict__ parts,
                                                                              int n_parts, const T* __restrict__ w,
                                                                              T* __restrict__ out, int64_t rows,
                                                                              int cols, float eps) {
     constexpr int N = Vec<T>::N;
+    constexpr bool kHold = NP > 0 && CH * NP * N <= 128;  // partials held in registers
+    constexpr int NH = kHold ? NP : 1;
     __shared__ float part[kRowThreads / 64];
     const int64_t row = blockIdx.x;
     const int nch = cols / N;
     T* xr = x + row * cols;
     uint4 c[CH], wc[CH];
+    float4 pq[kHold ? CH : 1][NH][N / 4];
+#pragma unroll
+    for (int i = 0; i < CH; ++i) {
+        const int idx = i * kRowThreads + (int)threadIdx.x;
+        if (idx < nch) {
+            c[i] = ld16<true>(xr + idx * N);
+            if (w) wc[i] = ld16<false>(w + idx * N);
+            if constexpr (kHold) {
+#pragma unroll
+                for (int sp = 0; sp < NP; ++sp) {
+                    const float* pp = parts + ((int64_t)sp * rows + row) * cols + (int64_t)idx * N;
+#pragma unroll
+                    for (int e = 0; e < N; e += 4) pq[i][sp][e / 4] = *reinterpret_cast<const float4*>(pp + e);
+                }
+            }
+        }
+    }
     float ss = 0.f;
 #pragma unroll
     for (int i = 0; i < CH; ++i) {
         const int idx = i * kRowThreads + (int)threadIdx.x;
         if (idx < nch) {
-            uint4 a = ld16<true>(xr + idx * N);
-            if (w) wc[i] = ld16<false>(w + idx * N);
             float va[N], vh[N];
 #pragma unroll
             for (int e = 0; e < N; ++e) vh[e] = 0.f;
-            for (int sp = 0; sp < n_parts; ++sp) {
-                const float* pp = parts + ((int64_t)sp * rows + row) * cols + (int64_t)idx * N;
+            auto add4 = [&](int e, const float4 q) __attribute__((always_inline)) {
+                vh[e] += q.x;
+                vh[e + 1] += q.y;
+                vh[e + 2] += q.z;
+                vh[e + 3] += q.w;
+            };
+            if constexpr (kHold) {
 #pragma unroll
-                for (int e = 0; e < N; e += 4) {
-                    const float4 q = *reinterpret_cast<const float4*>(pp + e);
-                    vh[e] += q.x;
-                    vh[e + 1] += q.y;
-                    vh[e + 2] += q.z;
-                    vh[e + 3] += q.w;
+                for (int sp = 0; sp < NP; ++sp)
+#pragma unroll
+                    for (int e = 0; e < N; e += 4) add4(e, pq[i][sp][e / 4]);
+            } else {
+                for (int sp = 0; sp < n_parts; ++sp) {
+                    const float* pp = parts + ((int64_t)sp * rows + row) * cols + (int64_t)idx * N;
+#pragma unroll
+                    for (int e = 0; e < N; e += 4) add4(e, *reinterpret_cast<const float4*>(pp + e));
                 }
             }
-            Vec<T>::unpack(a, va);
+            Vec<T>::unpack(c[i], va);
 #pragma unroll
             for (int e = 0; e < N; ++e) va[e] += rt<T>(vh[e]);
-            a = Vec<T>::pack(va);
+            const uint4 a = Vec<T>::pack(va);
             st16<true>(xr + idx * N, a);
             c[i] = a;
             float v[N];
@@ -304,8 +341,15 @@ int launch_add_parts_norm(T* x, const float* parts, int n_parts, const T* w, T* 
     const int per_thread = (cols / Vec<T>::N + kRowThreads - 1) / kRowThreads;
 #define CRANE_PARTS_CASE(ch)                                                                                      \
     if (per_thread <= ch) {                                                                                       \
-        hipLaunchKernelGGL((add_parts_rms_norm_row_kernel<T, ch>), dim3((unsigned)rows), dim3(kRowThreads), 0, st, \
-                           x, parts, n_parts, w, out, rows, cols, eps);                                           \
+        if (n_parts == 4)                                                                                         \
+            hipLaunchKernelGGL((add_parts_rms_norm_row_kernel<T, ch, 4>), dim3((unsigned)rows), dim3(kRowThreads), \
+                               0, st, x, parts, n_parts, w, out, rows, cols, eps);                                \
+        else if (n_parts == 2)                                                                                    \
+            hipLaunchKernelGGL((add_parts_rms_norm_row_kernel<T, ch, 2>), dim3((unsigned)rows), dim3(kRowThreads), \
+                               0, st, x, parts, n_parts, w, out, rows, cols, eps);                                \
+        else                                                                                                      \
+            hipLaunchKernelGGL((add_parts_rms_norm_row_kernel<T, ch, 0>), dim3((unsigned)rows), dim3(kRowThreads), \
+                               0, st, x, parts, n_parts, w, out, rows, cols, eps);                                \
         return launch_status(hipGetLastError());                                                                  \
     }
     CRANE_PARTS_CASE(1)
