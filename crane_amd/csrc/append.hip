@@ -37,23 +37,16 @@ __device__ __forceinline__ float group8_sum(float x) {
 // x / m * w in T) or the LayerNorm fallback used for a non-contiguous input
 // (x / sqrt(mean(x^2)+eps) in f32, converted to T, then * w in T).  The sum of
 // squares accumulates in f32.
+// w1, w2: this lane's 16 weights (the caller loads them with the row).
 template <typename T>
-__device__ __forceinline__ void rms_norm8(float (&x1)[8], float (&x2)[8], const T* w, int l, float eps,
-                                          bool contiguous) {
+__device__ __forceinline__ void rms_norm8(float (&x1)[8], float (&x2)[8], const float (&w1)[8],
+                                          const float (&w2)[8], float eps, bool contiguous) {
     float ss = 0.f;
 #pragma unroll
     for (int i = 0; i < 8; ++i) ss += x1[i] * x1[i] + x2[i] * x2[i];
     ss = group8_sum(ss);
     float m = sqrtf(ss * (1.0f / kHeadDim) + eps);
     if (contiguous) m = rt<T>(m);
-    float w1[8], w2[8];
-    if (w) {
-        load8(w + 8 * l, w1);
-        load8(w + 64 + 8 * l, w2);
-    } else {
-#pragma unroll
-        for (int i = 0; i < 8; ++i) w1[i] = w2[i] = 1.f;
-    }
     // x / m from one reciprocal per row (div_by) when every row of the wave has
     // a normal, moderate m (m >= sqrt(eps) is never 0 for eps > 0); the
     // division otherwise (an infinite or NaN input, a zero eps)
@@ -101,30 +94,46 @@ __global__ __launch_bounds__(256) void qknorm_rope_append_kernel(
     const int s = (int)(tok % S);
     const int b = (int)(tok / S);
 
+    const bool is_q = head < Hq, is_v = head >= Hq + Hkv;
+    // Every load that does not wait on another is issued first: the row, the
+    // lengths and the norm weights; only the cos / sin rows wait on the
+    // position.  Only k and v heads read cache_len, which the q-only entry
+    // point (crane_hip_qnorm_rope) does not pass: q heads read positions in
+    // its place (a load with no branch around it, so nothing waits for it).
+    const int32_t cl_raw = (is_q ? positions : cache_len)[b];
+    const int32_t cl = is_q ? 0 : cl_raw;
+    const int32_t pb = positions[b];
     const T* src = qkv + tok * row_stride + (int64_t)head * kHeadDim;
     float x1[8], x2[8];
     load8(src + 8 * l, x1);
     load8(src + 64 + 8 * l, x2);
+    const T* w = is_q ? qw : kw;
+    float w1[8], w2[8];
+    if (!is_v && w) {
+        load8(w + 8 * l, w1);
+        load8(w + 64 + 8 * l, w2);
+    } else {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) w1[i] = w2[i] = 1.f;
+    }
 
-    if (head >= Hq + Hkv) {  // value row: straight into the cache
-        const int64_t off = rows.offset(b, Hkv, head - Hq - Hkv, (int64_t)cache_len[b] + s);
+    if (is_v) {  // value row: straight into the cache
+        const int64_t off = rows.offset(b, Hkv, head - Hq - Hkv, (int64_t)cl + s);
         if (off < 0) return;  // past the capacity (or on an invalid page): not written
         T* dst = v_cache + off;
         store8(dst + 8 * l, x1);
         store8(dst + 64 + 8 * l, x2);
         return;
     }
-    const bool is_q = head < Hq;
     T* dst;
     if (is_q) {
         dst = q_out + (((int64_t)b * Hq + head) * S + s) * kHeadDim;
     } else {
-        const int64_t off = rows.offset(b, Hkv, head - Hq, (int64_t)cache_len[b] + s);
+        const int64_t off = rows.offset(b, Hkv, head - Hq, (int64_t)cl + s);
         if (off < 0) return;
         dst = k_cache + off;
     }
-    const T* w = is_q ? qw : kw;
-    const int64_t p = (int64_t)positions[b] + s;
+    const int64_t p = (int64_t)pb + s;
     if (p < 0 || p >= table_rows) return;  // no table row for this position: nothing is written
     float c[8], sn[8];
     load8(cos_t + p * cs_stride + 8 * l, c);
@@ -132,9 +141,9 @@ __global__ __launch_bounds__(256) void qknorm_rope_append_kernel(
 
     // Qwen3 norms the transposed [B,H,S,D] view, contiguous only when S == 1;
     // Hunyuan norms the contiguous rope output.
-    if (order == CRANE_HIP_NORM_THEN_ROPE) rms_norm8(x1, x2, w, l, eps, S == 1);
+    if (order == CRANE_HIP_NORM_THEN_ROPE) rms_norm8<T>(x1, x2, w1, w2, eps, S == 1);
     rope8<T>(x1, x2, c, sn);
-    if (order == CRANE_HIP_ROPE_THEN_NORM) rms_norm8(x1, x2, w, l, eps, true);
+    if (order == CRANE_HIP_ROPE_THEN_NORM) rms_norm8<T>(x1, x2, w1, w2, eps, true);
 
     store8(dst + 8 * l, x1);
     store8(dst + 64 + 8 * l, x2);
