@@ -317,7 +317,7 @@ __global__ __launch_bounds__(kThreads) void topk_kernel(const float* __restrict_
 //            k-th largest of the P slice maxima -- k elements of distinct
 //            slices are >= t, so t is a lower bound of the row's k-th largest
 //            and every answer has a key >= t (t is taken a little lower
-//            still, to the 16-bit prefix) -- and appends its slice's keys
+//            still, to the 24-bit prefix) -- and appends its slice's keys
 //            >= t to the row's candidate list (wave-aggregated atomics);
 //            (3) one workgroup per row ranks the candidates (a few hundred for
 //            real logits; a thread's rank is the count of larger candidates)
@@ -427,16 +427,18 @@ __global__ __launch_bounds__(kSplitThreads) void topk_max_kernel(const float* __
 
 // A lower bound of the k-th largest of the P (<= kSplitMaxParts) keys
 // m[0..P), by one wave: the largest t with at least k keys >= t, bit by bit
-// over the top 16 bits only (t's low 16 bits are 0).  It lies within the
-// k-th largest key's 16-bit prefix, so it admits at most the few extra keys
-// that share that prefix (none for logits widened from bf16), in half the
-// steps of the exact search.
+// over the top 24 bits only (t's low 8 bits are 0).  It lies within the k-th
+// largest key's 24-bit prefix (2^-15 of its value), so it admits at most the
+// few extra keys that share that prefix (none for logits widened from bf16),
+// in three quarters of the steps of the exact search.  (A 16-bit prefix,
+// 2^-7 of the value, takes the same time here but lets a row whose values
+// crowd near the k-th overflow the candidate list.)
 __device__ __forceinline__ uint32_t kth_largest_wave(const uint32_t* m, int P, int k, int lane) {
     uint32_t v[kSplitMaxParts / 64];
 #pragma unroll
     for (int j = 0; j < kSplitMaxParts / 64; ++j) v[j] = 64 * j + lane < P ? m[64 * j + lane] : 0u;
     uint32_t t = 0;
-    for (int bit = 31; bit >= 16; --bit) {
+    for (int bit = 31; bit >= 8; --bit) {
         const uint32_t c = t | (1u << bit);
         int cnt = 0;
 #pragma unroll

@@ -179,6 +179,24 @@ def test_split_rows_ties_masks_and_nan(gpu, orc):
 
 
 @pytest.mark.gpu
+def test_split_topk_crowded_values(gpu, orc):
+    """Rows whose values all lie within 2^-8 of 1 (every key shares its top 16
+    bits): the split top-k's threshold, a 24-bit prefix of the k-th largest
+    slice maximum, still bounds the answer, and the result is the oracle's,
+    at one row and at a batch."""
+    from crane_amd import ops
+    n = VOCAB
+    rng = np.random.default_rng(77)
+    x = (np.float32(1.0) + rng.uniform(0.0, 2.0 ** -8, size=(3, n)).astype(np.float32)).astype(np.float32)
+    x[2, 5000:5100] = x[2, 5000]                  # and a run of equal values among them
+    for rows in (1, 3):
+        for k in (64, 7):
+            print(f"crowded values: rows {rows} k={k}", flush=True)
+            got = ops.topk_indices(_t(x[:rows], "f32", gpu), k).cpu().numpy().astype(np.uint32)
+            np.testing.assert_array_equal(got, orc.topk(x[:rows], k), err_msg=f"rows={rows} k={k}")
+
+
+@pytest.mark.gpu
 def test_split_workspace_shared_across_calls(gpu):
     """One workspace (filled with garbage first) serves argmax and top-k calls
     of different row counts in any order: it holds nothing between calls."""
