@@ -147,32 +147,6 @@ __device__ __forceinline__ void decode_item(
     auto& red = sm.red;
     auto& ml = sm.ml;
 
-    // Grouped path: q_g = q * scale in T, for this lane's 16 dims of every head.
-    // Standard path: q as is (q * 1 rounds to q itself).
-    const float scale_t = rt<T>(scale);
-    const float qmul = post ? 1.0f : scale_t;
-    uint32_t qp[kBf16 ? G : 1][8];
-    float qf[kBf16 ? 1 : G][16];
-#pragma unroll
-    for (int h = 0; h < G; ++h) {
-        float x[16];
-        // the lane's dims are those of its K pieces: bytes [128 v + 16 a8, +16) of the row
-        const T* qr = q + ((int64_t)b * Hq + h0 + h) * kHeadDim;
-        if constexpr (kBf16) {
-            load8(qr + 8 * a8, *reinterpret_cast<float(*)[8]>(&x[0]));
-            load8(qr + 64 + 8 * a8, *reinterpret_cast<float(*)[8]>(&x[8]));
-        } else {
-#pragma unroll
-            for (int v = 0; v < 4; ++v) load4(qr + 32 * v + 4 * a8, *reinterpret_cast<float(*)[4]>(&x[4 * v]));
-        }
-        if constexpr (kBf16) {
-#pragma unroll
-            for (int i = 0; i < 8; ++i) qp[h][i] = pack_bf16x2(x[2 * i] * qmul, x[2 * i + 1] * qmul);
-        } else {
-#pragma unroll
-            for (int i = 0; i < 16; ++i) qf[h][i] = x[i] * qmul;
-        }
-    }
     // Rows [j0, j0 + n) of this (sequence, kv head), contiguous in both
     // layouts (a page holds whole chunks); loads past them return 0, and so
     // do all of them for a page id outside the pool.
@@ -182,39 +156,80 @@ __device__ __forceinline__ void decode_item(
     const __amdgpu_buffer_rsrc_t rv = make_rsrc(vc + (off < 0 ? 0 : off), nbytes);
     constexpr int kRowBytes = kHeadDim * (int)sizeof(T);
 
-    // ---- A: raw scores q_g . k; wave w owns keys [w CH/4, (w+1) CH/4), 8 per load instruction
+    // q's pieces, then the first kKRows K row steps, are all issued before
+    // any of them is used (the scheduling barrier keeps q's unpacking behind
+    // the K loads), so q's round trip and the first K rows' overlap.
+    // The lane's q dims are those of its K pieces: bytes [128 v + 16 a8, +16)
+    // of the row.
+    constexpr int kQPieces = 16 * (int)sizeof(T) / 16;  // 16-byte pieces per lane and head
+    uint4 qraw[G][kQPieces];
 #pragma unroll
-    for (int half = 0; half < kStepsA / kKRows; ++half) {
-        uint4 kr[kKRows][kVecA];
+    for (int h = 0; h < G; ++h) {
+        const T* qr = q + ((int64_t)b * Hq + h0 + h) * kHeadDim;
 #pragma unroll
-        for (int t = 0; t < kKRows; ++t) {
-            const int j = wave * (CH / 4) + (half * kKRows + t) * 8 + r8;
+        for (int v = 0; v < kQPieces; ++v)
+            qraw[h][v] = *reinterpret_cast<const uint4*>(qr + (128 * v + 16 * a8) / (int)sizeof(T));
+    }
+    uint4 kr[kKRows][kVecA];
+    auto k_load = [&](int step, int slot) __attribute__((always_inline)) {
+        const int j = wave * (CH / 4) + step * 8 + r8;
 #pragma unroll
-            for (int v = 0; v < kVecA; ++v) kr[t][v] = buf_load16(rk, j * kRowBytes + 128 * v + 16 * a8);
-        }
+        for (int v = 0; v < kVecA; ++v) kr[slot][v] = buf_load16(rk, j * kRowBytes + 128 * v + 16 * a8);
+    };
 #pragma unroll
-        for (int t = 0; t < kKRows; ++t) {
-            const int j = wave * (CH / 4) + (half * kKRows + t) * 8 + r8;
-            float acc[G];
+    for (int t = 0; t < kKRows; ++t) k_load(t, t);
+    __builtin_amdgcn_sched_barrier(0);
+
+    // Grouped path: q_g = q * scale in T, for this lane's 16 dims of every head.
+    // Standard path: q as is (q * 1 rounds to q itself).
+    const float scale_t = rt<T>(scale);
+    const float qmul = post ? 1.0f : scale_t;
+    uint32_t qp[kBf16 ? G : 1][8];
+    float qf[kBf16 ? 1 : G][16];
 #pragma unroll
-            for (int h = 0; h < G; ++h) {
-                float a = 0.f;
-                if constexpr (kBf16) {
-                    const uint32_t* kw = reinterpret_cast<const uint32_t*>(&kr[t][0]);
+    for (int h = 0; h < G; ++h) {
+        float x[16];
+        const uint32_t* w = reinterpret_cast<const uint32_t*>(&qraw[h][0]);
+        if constexpr (kBf16) {
 #pragma unroll
-                    for (int i = 0; i < 8; ++i) a = dot2(qp[h][i], kw[i], a);
-                } else {
-                    const float* kf = reinterpret_cast<const float*>(&kr[t][0]);
-#pragma unroll
-                    for (int i = 0; i < 16; ++i) a += qf[h][i] * kf[i];
-                }
-                acc[h] = row8_sum(a);
+            for (int i = 0; i < 8; ++i) {
+                x[2 * i] = bf16_lo(w[i]);
+                x[2 * i + 1] = bf16_hi(w[i]);
             }
-            float mine = acc[0];
 #pragma unroll
-            for (int h = 1; h < G; ++h) mine = a8 == h ? acc[h] : mine;
-            if (a8 < G && j < n) s_lds[a8][j] = mine;
+            for (int i = 0; i < 8; ++i) qp[h][i] = pack_bf16x2(x[2 * i] * qmul, x[2 * i + 1] * qmul);
+        } else {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) qf[h][i] = __uint_as_float(w[i]) * qmul;
         }
+    }
+    // ---- A: raw scores q_g . k; wave w owns keys [w CH/4, (w+1) CH/4), 8 per
+    // load instruction, through a ring of kKRows row steps, each refilled with
+    // the step kKRows ahead as soon as it is used (no drain between groups)
+#pragma unroll
+    for (int step = 0; step < kStepsA; ++step) {
+        const int t = step % kKRows;
+        const int j = wave * (CH / 4) + step * 8 + r8;
+        float acc[G];
+#pragma unroll
+        for (int h = 0; h < G; ++h) {
+            float a = 0.f;
+            if constexpr (kBf16) {
+                const uint32_t* kw = reinterpret_cast<const uint32_t*>(&kr[t][0]);
+#pragma unroll
+                for (int i = 0; i < 8; ++i) a = dot2(qp[h][i], kw[i], a);
+            } else {
+                const float* kf = reinterpret_cast<const float*>(&kr[t][0]);
+#pragma unroll
+                for (int i = 0; i < 16; ++i) a += qf[h][i] * kf[i];
+            }
+            acc[h] = row8_sum(a);
+        }
+        float mine = acc[0];
+#pragma unroll
+        for (int h = 1; h < G; ++h) mine = a8 == h ? acc[h] : mine;
+        if (a8 < G && j < n) s_lds[a8][j] = mine;
+        if (step + kKRows < kStepsA) k_load(step + kKRows, t);
     }
 
     // Prefetch this lane's first V row pairs for C while B runs: pair m =
