@@ -203,6 +203,21 @@ __device__ __forceinline__ void decode_item(
             for (int i = 0; i < 16; ++i) qf[h][i] = __uint_as_float(w[i]) * qmul;
         }
     }
+    // This lane's first V row pairs for C: ring slot t holds pair m =
+    // w CH/8 + 4t + grp, rows 2m and 2m+1.  The first kVEarly slots are
+    // issued during A's last steps, each as a K slot frees up (a V slot takes
+    // the registers of a K slot), the others after A.
+    uint4 vr[kVRing][2][kVecC];
+    auto v_load = [&](int t) __attribute__((always_inline)) {
+        const int m = wave * (CH / 8) + 4 * t + grp;
+#pragma unroll
+        for (int r = 0; r < 2; ++r)
+#pragma unroll
+            for (int v = 0; v < kVecC; ++v)
+                vr[t][r][v] = buf_load16(rv, (2 * m + r) * kRowBytes + 16 * (kVecC * l16 + v));
+    };
+    constexpr int kVEarly = kKRows < kVRing ? kKRows : kVRing;
+
     // ---- A: raw scores q_g . k; wave w owns keys [w CH/4, (w+1) CH/4), 8 per
     // load instruction, through a ring of kKRows row steps, each refilled with
     // the step kKRows ahead as soon as it is used (no drain between groups)
@@ -230,20 +245,12 @@ __device__ __forceinline__ void decode_item(
         for (int h = 1; h < G; ++h) mine = a8 == h ? acc[h] : mine;
         if (a8 < G && j < n) s_lds[a8][j] = mine;
         if (step + kKRows < kStepsA) k_load(step + kKRows, t);
+        else if (step + kKRows - kStepsA < kVEarly) v_load(step + kKRows - kStepsA);
     }
 
-    // Prefetch this lane's first V row pairs for C while B runs: pair m =
-    // w CH/8 + 4t + grp is rows 2m and 2m+1.
-    uint4 vr[kVRing][2][kVecC];
+    // The rest of the V ring's first fill, in flight while B runs.
 #pragma unroll
-    for (int t = 0; t < kVRing; ++t) {
-        const int m = wave * (CH / 8) + 4 * t + grp;
-#pragma unroll
-        for (int r = 0; r < 2; ++r)
-#pragma unroll
-            for (int v = 0; v < kVecC; ++v)
-                vr[t][r][v] = buf_load16(rv, (2 * m + r) * kRowBytes + 16 * (kVecC * l16 + v));
-    }
+    for (int t = kVEarly; t < kVRing; ++t) v_load(t);
     __syncthreads();
 
     // ---- B: per-head chunk max and sum; probabilities to LDS
