@@ -524,23 +524,34 @@ int launch_ring(const RingCfg& c, const bf16_t* x, const bf16_t* w, const bf16_t
     return launch_status(hipGetLastError());
 }
 
-// Split-K partial products (decode rows, M <= 32): 64 features (FT 4) and 4
-// waves per workgroup, K cut into `splits` ranges over gridDim.y, each wave's
-// quarter of its range walked in 128-wide stages through a ring of 2 slots
-// (128 KiB of LDS: one workgroup per CU).  The ring depth, or 0 when the
-// shape does not split this way.
+// Split-K partial products (decode rows, M <= 32): 64 features (FT 4) per
+// workgroup, K cut into `splits` ranges over gridDim.y, each wave's part of
+// its range walked in 128-wide stages through a ring of its own.  Two forms,
+// one workgroup per CU either way: 2 waves and a ring of 3 slots (96 KiB of
+// LDS) when each wave's stage count is a multiple of 3, else 4 waves and a
+// ring of 2 (128 KiB).  (The ring loop needs the stage count a multiple of
+// the depth; 4 slots of FT 4 would pass the 6-bit vmcnt.)  Qwen3-8B down_proj
+// [4096 x 12288] in 4 splits: 20.0 -> 19.4 us with the ring of 3; o_proj
+// [4096 x 4096] (4 stages per wave) keeps the ring of 2.  The ring depth of
+// the form a shape takes, or 0 when the shape does not split this way.
 int split_ring_depth(int64_t M, int64_t N, int64_t K, int64_t splits) {
     if (M < 1 || M > kSkMaxM || N < 64 || N % 64 || N > 0x7fffffff || splits < 2 || splits > 16) return 0;
     if (K % (splits * 4 * 256)) return 0;  // whole ring turns: 2 stages of 128 per wave
     if (K / splits / 4 > kRingMaxK || 16LL * 4 * K * 2 > 0xffffffffLL) return 0;
-    return 2;
+    const int64_t nst2 = K / splits / 2 / 128;  // stages per wave with 2 waves
+    return nst2 % 3 == 0 && K / splits / 2 <= kRingMaxK ? 3 : 2;
 }
 
 template <int MT>
-void launch_split(const bf16_t* x, const bf16_t* w, float* part, int M, int N, int K, int splits, hipStream_t st) {
-    const dim3 grid((unsigned)(N / 64), (unsigned)splits), block(256);
-    hipLaunchKernelGGL((ring_gemm_kernel<MT, 4, 2, 4, false, false, true>), grid, block, 0, st, x, w, nullptr,
-                       nullptr, M, N, K, part);
+void launch_split(const bf16_t* x, const bf16_t* w, float* part, int M, int N, int K, int splits, int depth,
+                  hipStream_t st) {
+    const dim3 grid((unsigned)(N / 64), (unsigned)splits);
+    if (depth == 3)
+        hipLaunchKernelGGL((ring_gemm_kernel<MT, 2, 3, 4, false, false, true>), grid, dim3(128), 0, st, x, w, nullptr,
+                           nullptr, M, N, K, part);
+    else
+        hipLaunchKernelGGL((ring_gemm_kernel<MT, 4, 2, 4, false, false, true>), grid, dim3(256), 0, st, x, w, nullptr,
+                           nullptr, M, N, K, part);
 }
 
 struct Plan {
@@ -736,13 +747,14 @@ extern "C" int crane_gemm_linear_split(crane_gemm* g, const void* x, const void*
     if (M == 0) return CRANE_HIP_OK;
     if (!x || !w || !part) return CRANE_HIP_E_INVALID;
     if (!crane::aligned16(x) || !crane::aligned16(w) || !crane::aligned16(part)) return CRANE_HIP_E_ALIGN;
-    if (dtype != CRANE_HIP_BF16 || !crane::split_ring_depth(M, N, K, splits)) return CRANE_HIP_E_INVALID;
+    const int depth = dtype == CRANE_HIP_BF16 ? crane::split_ring_depth(M, N, K, splits) : 0;
+    if (!depth) return CRANE_HIP_E_INVALID;
     hipStream_t st = (hipStream_t)stream;
     if (M <= 16)
         crane::launch_split<1>((const crane::bf16_t*)x, (const crane::bf16_t*)w, part, (int)M, (int)N, (int)K, splits,
-                               st);
+                               depth, st);
     else
         crane::launch_split<2>((const crane::bf16_t*)x, (const crane::bf16_t*)w, part, (int)M, (int)N, (int)K, splits,
-                               st);
+                               depth, st);
     return crane::launch_status(hipGetLastError());
 }

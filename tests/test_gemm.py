@@ -199,10 +199,12 @@ def test_split_shape_query():
 @pytest.mark.gpu
 @pytest.mark.parametrize("M,N,K,splits", [
     (32, 4096, 4096, 4),    # o_proj at the c3 decode batch: 64 workgroups x 4 splits
-    (32, 4096, 12288, 4),   # down_proj at c3: 6 stages a wave
+    (32, 4096, 12288, 4),   # down_proj at c3: 2 waves, 12 stages a wave through a ring of 3
     (5, 1024, 2048, 2),     # one token group; one ring turn a wave
     (17, 256, 8192, 8),     # a partial second token group, 8 splits
     (1, 640, 3072, 3),      # one token row, 3 splits
+    (9, 512, 6144, 2),      # one token group, ring of 3
+    (20, 320, 9216, 3),     # a partial second token group, 5 feature tiles, ring of 3
 ])
 def test_linear_split_parity(gpu, orc, M, N, K, splits):
     """The f32 partial products of crane_gemm_linear_split, summed in split
