@@ -437,6 +437,46 @@ def bench_sampling(args, dev, stream, lib):
     return res
 
 
+def bench_read_ceiling(args, dev, stream):
+    """The HBM read rate this GPU reaches with the decode kernel's access
+    pattern: crane_amd's libcrane_probe.so (a measurement helper beside the
+    library, not part of it) reads 3 rotated buffers of the config 3 decode's
+    bytes per call (320 MB, past the 256 MB Infinity Cache), one workgroup per
+    contiguous span with all of the span's loads in flight, at 8, 16 and 32
+    loads per thread (32-128 KiB spans); the fastest is the ceiling the decode
+    call is compared with.  None when the probe library is not built."""
+    import ctypes
+    import torch
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "crane_amd", "libcrane_probe.so")
+    if not os.path.exists(path):
+        log("[read ceiling] libcrane_probe.so not built: skipped")
+        return None
+    probe = ctypes.CDLL(path)
+    probe.crane_probe_read.restype = ctypes.c_int
+    probe.crane_probe_read.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p]
+    probe.crane_probe_workgroups.restype = ctypes.c_int64
+    probe.crane_probe_workgroups.argtypes = [ctypes.c_int64, ctypes.c_int]
+    nbytes, R = 320 * 1000 * 1000, 3
+    bufs = [torch.ones(nbytes // 4, dtype=torch.int32, device=dev) for _ in range(R)]
+    sink = torch.empty(int(probe.crane_probe_workgroups(nbytes, 8)), dtype=torch.int32, device=dev)
+    st = stream.cuda_stream
+    best = None
+    for loads in (8, 16, 32):
+        def launch(i, loads=loads):
+            rc = probe.crane_probe_read(bufs[i % R].data_ptr(), nbytes, sink.data_ptr(), loads, st)
+            if rc:
+                raise RuntimeError(f"crane_probe_read failed: {rc}")
+        ms = timed(launch, args.steps, args.warmup, stream)
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        log(f"[read ceiling] {16 * 256 * loads // 1024} KiB per workgroup: {ms * 1e3:.2f} us per 320 MB, "
+            f"{gbs:.1f} GB/s ({gbs / HBM_PEAK_GBS * 100:.1f}% of HBM)")
+        if best is None or gbs > best["gbs"]:
+            best = dict(gbs=gbs, ms=ms, span_kib=16 * 256 * loads // 1024)
+    del bufs
+    torch.cuda.empty_cache()
+    return best
+
+
 # ---------------------------------------------------------------- prefill
 
 def bench_prefill(args, dev, stream, lib):
@@ -836,8 +876,10 @@ def main():
         del src, dst
         torch.cuda.empty_cache()
     dec = pre = c5 = c2 = app = pg = pf32 = None
+    ceil = None
     if args.only in ("decode", "all"):
         dec = bench_decode(args, dev, stream, lib)
+        ceil = bench_read_ceiling(args, dev, stream)
         if args.only == "all":
             c5 = bench_decode_c5(args, dev, stream, lib)
             pg = bench_decode_paged(args, dev, stream, lib)
@@ -878,6 +920,16 @@ def main():
                          "event-timed launches after the timed region; value_p50: GB/s at that median",
             "value_p50": round(dec["algo_bytes"] / (dec["pct"][1] * 1e-3) / 1e9, 2),
         })
+        if ceil is not None:
+            line["hbm_read_ceiling"] = {
+                "gbs": round(ceil["gbs"], 1), "frac_of_peak": round(ceil["gbs"] / HBM_PEAK_GBS, 4),
+                "span_kib_per_workgroup": ceil["span_kib"], "bytes_per_launch": 320 * 1000 * 1000,
+                "decode_frac_of_ceiling": round(dec["gbs"] / ceil["gbs"], 4),
+                "decode_p50_frac_of_ceiling": round(line["value_p50"] / ceil["gbs"], 4),
+                "note": "a read-only stream with the decode kernel's access pattern and load form "
+                        "(crane_amd/csrc/probe/hbm_probe.hip, a measurement helper outside the library: one "
+                        "workgroup per contiguous span, all its loads in flight), 3 rotated 320 MB buffers; the "
+                        "decode roofline's peak stays the 8 TB/s datasheet figure"}
     if pre is not None:
         pre_obj = {"metric": "prefill attn TFLOP/s (c4: Qwen2.5-7B shape, B=8, S=4096, 28/4 heads, causal, bf16)",
                    "value": round(pre["tflops"], 2), "unit": "TFLOP/s", "ms_per_step": round(pre["ms"], 4),

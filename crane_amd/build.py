@@ -15,6 +15,9 @@ CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libcrane_hip.so")
 SOURCES = ["capi.hip", "rope.hip", "append.hip", "decode.hip", "prefill.hip", "kvcache.hip", "pagedkv.hip", "layer.hip", "gemm.hip", "sampling.hip"]
+# bench.py's HBM read-rate probe: a separate library, not part of the C ABI
+PROBE_SRC = os.path.join(CSRC, "probe", "hbm_probe.hip")
+PROBE_LIB = os.path.join(HERE, "libcrane_probe.so")
 
 ARCH = "gfx950"
 # -packed-fp32-ops: no v_pk_{add,mul,fma}_f32 in any kernel.
@@ -51,8 +54,14 @@ def build(verbose: bool = True) -> str:
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{' '.join(cmd)}\n{r.stdout}\n{r.stderr}")
     os.replace(tmp, LIB)
+    tmp = PROBE_LIB + ".tmp"
+    cmd = [hipcc(), *HIPFLAGS, "-shared", "-o", tmp, PROBE_SRC]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"hipcc failed for the probe:\n{' '.join(cmd)}\n{r.stdout}\n{r.stderr}")
+    os.replace(tmp, PROBE_LIB)
     if verbose:
-        print(f"built {LIB}")
+        print(f"built {LIB} and {PROBE_LIB}")
     return LIB
 
 
