@@ -33,6 +33,9 @@ SIGNATURES = {
     "crane_hip_qknorm_rope_append": (
         [_vp, _i64, _vp, _vp, _f, _i, _vp, _vp, _i64, _i64, _i32p, _vp, _vp, _vp, _i64, _i32p, _i64,
          _i, _i, _i, _i, _i, _i, _vp], _i),
+    "crane_hip_qknorm_rope_append_parts": (
+        [_vp, _i, _vp, _vp, _vp, _f, _i, _vp, _vp, _i64, _i64, _i32p, _vp, _vp, _vp, _i64, _i32p, _i64,
+         _i, _i, _i, _i, _i, _i, _vp], _i),
     "crane_hip_qnorm_rope": (
         [_vp, _i64, _vp, _f, _i, _vp, _vp, _i64, _i64, _i32p, _vp, _i, _i, _i, _i, _i, _vp], _i),
     "crane_hip_rope_tables": ([_i, ctypes.c_double, ctypes.c_double, _i64, _i, _vp, _vp], _i),

@@ -41,9 +41,14 @@ __device__ __forceinline__ float group8_sum(float x) {
 template <typename T>
 __device__ __forceinline__ void rms_norm8(float (&x1)[8], float (&x2)[8], const float (&w1)[8],
                                           const float (&w2)[8], float eps, bool contiguous) {
+    // explicit FMAs: the sum's bits do not depend on how the compiler
+    // contracts it in each instantiation of the kernel
     float ss = 0.f;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) ss += x1[i] * x1[i] + x2[i] * x2[i];
+    for (int i = 0; i < 8; ++i) {
+        ss = __builtin_fmaf(x1[i], x1[i], ss);
+        ss = __builtin_fmaf(x2[i], x2[i], ss);
+    }
     ss = group8_sum(ss);
     float m = sqrtf(ss * (1.0f / kHeadDim) + eps);
     if (contiguous) m = rt<T>(m);
@@ -78,9 +83,62 @@ __device__ __forceinline__ void rope8(float (&x1)[8], float (&x2)[8], const floa
     }
 }
 
-template <typename T, class ROWS>
+// Where a head row comes from.  QkvRows: the merged projection's output
+// rows (row r at qkv + r * stride elements).  QkvParts: the f32 split-K
+// partial products of that projection [NP][rows][n] (crane_gemm_linear_split),
+// summed in split order, plus the bias when there is one, and rounded once
+// to T -- the rounding point of the whole product's output.  Both put the
+// lane's 16 values (dims 8 l.. and 64 + 8 l..) in x1, x2 and issue every load
+// before the first use.
+template <typename T>
+struct QkvRows {
+    const T* qkv;
+    int64_t stride;
+    __device__ __forceinline__ void load(int64_t tok, int head, int l, float (&x1)[8], float (&x2)[8]) const {
+        const T* src = qkv + tok * stride + (int64_t)head * kHeadDim;
+        load8(src + 8 * l, x1);
+        load8(src + 64 + 8 * l, x2);
+    }
+};
+
+template <typename T, int NP>
+struct QkvParts {
+    const float* parts;
+    int64_t plane;  // elements per split: rows * n
+    int64_t n;      // elements per row: (Hq + 2 Hkv) D
+    const T* bias;  // [n] or null
+    __device__ __forceinline__ void load(int64_t tok, int head, int l, float (&x1)[8], float (&x2)[8]) const {
+        const float* src = parts + tok * n + (int64_t)head * kHeadDim;
+        float p1[NP][8], p2[NP][8], b1[8], b2[8];
+#pragma unroll
+        for (int sp = 0; sp < NP; ++sp) {
+            load8(src + sp * plane + 8 * l, p1[sp]);
+            load8(src + sp * plane + 64 + 8 * l, p2[sp]);
+        }
+        if (bias) {
+            load8(bias + (int64_t)head * kHeadDim + 8 * l, b1);
+            load8(bias + (int64_t)head * kHeadDim + 64 + 8 * l, b2);
+        } else {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) b1[i] = b2[i] = 0.f;
+        }
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            float a = 0.f, c = 0.f;
+#pragma unroll
+            for (int sp = 0; sp < NP; ++sp) {
+                a += p1[sp][i];
+                c += p2[sp][i];
+            }
+            x1[i] = rt<T>(a + b1[i]);
+            x2[i] = rt<T>(c + b2[i]);
+        }
+    }
+};
+
+template <typename T, class ROWS, class SRC>
 __global__ __launch_bounds__(256) void qknorm_rope_append_kernel(
-    const T* __restrict__ qkv, int64_t row_stride, const T* __restrict__ qw, const T* __restrict__ kw,
+    SRC src_rows, const T* __restrict__ qw, const T* __restrict__ kw,
     float eps, int order, const T* __restrict__ cos_t, const T* __restrict__ sin_t, int64_t cs_stride,
     int64_t table_rows, const int32_t* __restrict__ positions, T* __restrict__ q_out, T* __restrict__ k_cache,
     T* __restrict__ v_cache, ROWS rows, const int32_t* __restrict__ cache_len, int S, int Hq, int Hkv,
@@ -103,10 +161,8 @@ __global__ __launch_bounds__(256) void qknorm_rope_append_kernel(
     const int32_t cl_raw = (is_q ? positions : cache_len)[b];
     const int32_t cl = is_q ? 0 : cl_raw;
     const int32_t pb = positions[b];
-    const T* src = qkv + tok * row_stride + (int64_t)head * kHeadDim;
     float x1[8], x2[8];
-    load8(src + 8 * l, x1);
-    load8(src + 64 + 8 * l, x2);
+    src_rows.load(tok, head, l, x1, x2);
     const T* w = is_q ? qw : kw;
     float w1[8], w2[8];
     if (!is_v && w) {
@@ -149,10 +205,54 @@ __global__ __launch_bounds__(256) void qknorm_rope_append_kernel(
     store8(dst + 64 + 8 * l, x2);
 }
 
-// Checks shared by both layouts, then the launch; `rows` addresses the cache.
+// The rows an append reads: the projection's output rows (qkv, row stride
+// in elements) or its f32 split-K partial products (parts [n_parts][B S][n],
+// n_parts 2 or 4, and the projection's bias or null).
+struct RowSource {
+    const void* qkv = nullptr;
+    int64_t stride = 0;
+    const float* parts = nullptr;
+    int n_parts = 0;
+    const void* bias = nullptr;
+};
+
+template <typename T, class ROWS, class SRC>
+void launch_append(const SRC& src, int64_t blocks, const void* q_norm_w, const void* k_norm_w, float eps, int order,
+                   const void* cos, const void* sin, int64_t cs_stride, int64_t table_rows, const int32_t* positions,
+                   void* q_out, void* k_cache, void* v_cache, const ROWS& rows, const int32_t* cache_len, int S, int Hq,
+                   int Hkv, int64_t n_items, hipStream_t st) {
+    hipLaunchKernelGGL((qknorm_rope_append_kernel<T, ROWS, SRC>), dim3((unsigned)blocks), dim3(256), 0, st, src,
+                       (const T*)q_norm_w, (const T*)k_norm_w, eps, order, (const T*)cos, (const T*)sin, cs_stride,
+                       table_rows, positions, (T*)q_out, (T*)k_cache, (T*)v_cache, rows, cache_len, S, Hq, Hkv,
+                       n_items);
+}
+
+template <typename T, class ROWS>
+void launch_append_src(const RowSource& src, int64_t blocks, const void* q_norm_w, const void* k_norm_w, float eps,
+                       int order, const void* cos, const void* sin, int64_t cs_stride, int64_t table_rows,
+                       const int32_t* positions, void* q_out, void* k_cache, void* v_cache, const ROWS& rows,
+                       const int32_t* cache_len, int B, int S, int Hq, int Hkv, int64_t n_items, hipStream_t st) {
+    const int64_t n = (int64_t)(Hq + 2 * Hkv) * kHeadDim;
+    if (!src.parts) {
+        const QkvRows<T> r{(const T*)src.qkv, src.stride};
+        launch_append<T>(r, blocks, q_norm_w, k_norm_w, eps, order, cos, sin, cs_stride, table_rows, positions, q_out,
+                         k_cache, v_cache, rows, cache_len, S, Hq, Hkv, n_items, st);
+    } else if (src.n_parts == 2) {
+        const QkvParts<T, 2> r{src.parts, (int64_t)B * S * n, n, (const T*)src.bias};
+        launch_append<T>(r, blocks, q_norm_w, k_norm_w, eps, order, cos, sin, cs_stride, table_rows, positions, q_out,
+                         k_cache, v_cache, rows, cache_len, S, Hq, Hkv, n_items, st);
+    } else {
+        const QkvParts<T, 4> r{src.parts, (int64_t)B * S * n, n, (const T*)src.bias};
+        launch_append<T>(r, blocks, q_norm_w, k_norm_w, eps, order, cos, sin, cs_stride, table_rows, positions, q_out,
+                         k_cache, v_cache, rows, cache_len, S, Hq, Hkv, n_items, st);
+    }
+}
+
+// Checks shared by both layouts and both row sources, then the launch; `rows`
+// addresses the cache.
 template <class ROWS>
-int qknorm_rope_append(const void* qkv, int64_t qkv_row_stride, const void* q_norm_w, const void* k_norm_w,
-                       float eps, int order, const void* cos, const void* sin, int64_t cs_stride, int64_t table_rows,
+int qknorm_rope_append(const RowSource& src, const void* q_norm_w, const void* k_norm_w, float eps, int order,
+                       const void* cos, const void* sin, int64_t cs_stride, int64_t table_rows,
                        const int32_t* positions, void* q_out, void* k_cache, void* v_cache, const ROWS& rows,
                        const int32_t* cache_len, int B, int S, int Hq, int Hkv, int D, int dtype, void* stream) {
     if (dtype != CRANE_HIP_F32 && dtype != CRANE_HIP_BF16) return CRANE_HIP_E_DTYPE;
@@ -161,33 +261,29 @@ int qknorm_rope_append(const void* qkv, int64_t qkv_row_stride, const void* q_no
     if (Hq % Hkv != 0) return CRANE_HIP_E_GQA;
     if (order < CRANE_HIP_NORM_THEN_ROPE || order > CRANE_HIP_ROPE_ONLY) return CRANE_HIP_E_INVALID;
     if (!(eps >= 0.0f)) return CRANE_HIP_E_INVALID;
+    if (src.parts && src.n_parts != 2 && src.n_parts != 4) return CRANE_HIP_E_INVALID;
     if (B == 0 || S == 0) return CRANE_HIP_OK;
-    if (!qkv || !cos || !sin || !positions || !q_out || !k_cache || !v_cache || !cache_len)
+    if ((!src.parts && !src.qkv) || !cos || !sin || !positions || !q_out || !k_cache || !v_cache || !cache_len)
         return CRANE_HIP_E_INVALID;
-    if (qkv_row_stride < (int64_t)(Hq + 2 * Hkv) * D || cs_stride < D / 2 || table_rows <= 0)
-        return CRANE_HIP_E_INVALID;
+    if (cs_stride < D / 2 || table_rows <= 0) return CRANE_HIP_E_INVALID;
+    if (!src.parts && src.stride < (int64_t)(Hq + 2 * Hkv) * D) return CRANE_HIP_E_INVALID;
     const int64_t per16 = dtype == CRANE_HIP_BF16 ? 8 : 4;  // elements per 16 bytes
-    if (qkv_row_stride % per16 != 0 || cs_stride % per16 != 0) return CRANE_HIP_E_ALIGN;
-    if (!aligned16(qkv) || !aligned16(cos) || !aligned16(sin) || !aligned16(q_out) || !aligned16(k_cache) ||
-        !aligned16(v_cache) || (q_norm_w && !aligned16(q_norm_w)) || (k_norm_w && !aligned16(k_norm_w)))
+    if ((!src.parts && src.stride % per16 != 0) || cs_stride % per16 != 0) return CRANE_HIP_E_ALIGN;
+    if (!aligned16(src.parts ? (const void*)src.parts : src.qkv) || (src.bias && !aligned16(src.bias)) ||
+        !aligned16(cos) || !aligned16(sin) || !aligned16(q_out) || !aligned16(k_cache) || !aligned16(v_cache) ||
+        (q_norm_w && !aligned16(q_norm_w)) || (k_norm_w && !aligned16(k_norm_w)))
         return CRANE_HIP_E_ALIGN;
 
     const int64_t n_items = (int64_t)B * S * (Hq + 2 * Hkv);
     const int64_t blocks = (n_items + kItemsPerBlock - 1) / kItemsPerBlock;
     if (blocks > 0x7fffffffLL) return CRANE_HIP_E_INVALID;
     hipStream_t st = (hipStream_t)stream;
-    if (dtype == CRANE_HIP_F32) {
-        hipLaunchKernelGGL((qknorm_rope_append_kernel<float, ROWS>), dim3((unsigned)blocks), dim3(256), 0, st,
-                           (const float*)qkv, qkv_row_stride, (const float*)q_norm_w, (const float*)k_norm_w, eps,
-                           order, (const float*)cos, (const float*)sin, cs_stride, table_rows, positions, (float*)q_out,
-                           (float*)k_cache, (float*)v_cache, rows, cache_len, S, Hq, Hkv, n_items);
-    } else {
-        hipLaunchKernelGGL((qknorm_rope_append_kernel<bf16_t, ROWS>), dim3((unsigned)blocks), dim3(256), 0, st,
-                           (const bf16_t*)qkv, qkv_row_stride, (const bf16_t*)q_norm_w, (const bf16_t*)k_norm_w,
-                           eps, order, (const bf16_t*)cos, (const bf16_t*)sin, cs_stride, table_rows, positions,
-                           (bf16_t*)q_out, (bf16_t*)k_cache, (bf16_t*)v_cache, rows, cache_len, S, Hq, Hkv,
-                           n_items);
-    }
+    if (dtype == CRANE_HIP_F32)
+        launch_append_src<float>(src, blocks, q_norm_w, k_norm_w, eps, order, cos, sin, cs_stride, table_rows,
+                                 positions, q_out, k_cache, v_cache, rows, cache_len, B, S, Hq, Hkv, n_items, st);
+    else
+        launch_append_src<bf16_t>(src, blocks, q_norm_w, k_norm_w, eps, order, cos, sin, cs_stride, table_rows,
+                                  positions, q_out, k_cache, v_cache, rows, cache_len, B, S, Hq, Hkv, n_items, st);
     return launch_status(hipGetLastError());
 }
 
@@ -207,9 +303,33 @@ extern "C" int crane_hip_qknorm_rope_append(const void* qkv, int64_t qkv_row_str
     if (D != kHeadDim) return CRANE_HIP_E_HEAD_DIM;
     if (cache_cap <= 0 || max_rows < 0 || max_rows > cache_cap) return CRANE_HIP_E_CAPACITY;
     if ((int64_t)S > max_rows) return CRANE_HIP_E_CAPACITY;
-    return qknorm_rope_append(qkv, qkv_row_stride, q_norm_w, k_norm_w, eps, order, cos, sin, cs_stride, table_rows,
-                              positions, q_out, k_cache, v_cache, DenseRows{cache_cap}, cache_len, B, S, Hq, Hkv, D,
-                              dtype, stream);
+    RowSource src;
+    src.qkv = qkv;
+    src.stride = qkv_row_stride;
+    return qknorm_rope_append(src, q_norm_w, k_norm_w, eps, order, cos, sin, cs_stride, table_rows, positions, q_out,
+                              k_cache, v_cache, DenseRows{cache_cap}, cache_len, B, S, Hq, Hkv, D, dtype, stream);
+}
+
+// The same append reading the projection's split-K partial products: the
+// decode step's qkv_proj as crane_gemm_linear_split, its reduction (and bias)
+// folded into this pass.
+extern "C" int crane_hip_qknorm_rope_append_parts(const float* parts, int n_parts, const void* qkv_bias,
+                                                  const void* q_norm_w, const void* k_norm_w, float eps, int order,
+                                                  const void* cos, const void* sin, int64_t cs_stride,
+                                                  int64_t table_rows, const int32_t* positions, void* q_out,
+                                                  void* k_cache, void* v_cache, int64_t cache_cap,
+                                                  const int32_t* cache_len, int64_t max_rows, int B, int S, int Hq,
+                                                  int Hkv, int D, int dtype, void* stream) {
+    if (dtype != CRANE_HIP_F32 && dtype != CRANE_HIP_BF16) return CRANE_HIP_E_DTYPE;
+    if (D != kHeadDim) return CRANE_HIP_E_HEAD_DIM;
+    if (cache_cap <= 0 || max_rows < 0 || max_rows > cache_cap) return CRANE_HIP_E_CAPACITY;
+    if ((int64_t)S > max_rows) return CRANE_HIP_E_CAPACITY;
+    RowSource src;  // null parts: no rows at all (CRANE_HIP_E_INVALID unless nothing is to be done)
+    src.parts = parts;
+    src.n_parts = n_parts;
+    src.bias = qkv_bias;
+    return qknorm_rope_append(src, q_norm_w, k_norm_w, eps, order, cos, sin, cs_stride, table_rows, positions, q_out,
+                              k_cache, v_cache, DenseRows{cache_cap}, cache_len, B, S, Hq, Hkv, D, dtype, stream);
 }
 
 // The Hunyuan CLA layer (hunyuan_dense/modeling.rs:502-514) projects only q and
@@ -236,18 +356,14 @@ extern "C" int crane_hip_qnorm_rope(const void* q, int64_t q_row_stride, const v
     if (blocks > 0x7fffffffLL) return CRANE_HIP_E_INVALID;
     hipStream_t st = (hipStream_t)stream;
     const DenseRows none{1};  // never consulted: every item is a q head
-    if (dtype == CRANE_HIP_F32) {
-        hipLaunchKernelGGL((qknorm_rope_append_kernel<float, DenseRows>), dim3((unsigned)blocks), dim3(256), 0, st,
-                           (const float*)q, q_row_stride, (const float*)q_norm_w, (const float*)nullptr, eps, order,
-                           (const float*)cos, (const float*)sin, cs_stride, table_rows, positions, (float*)q_out,
-                           (float*)nullptr, (float*)nullptr, none, (const int32_t*)nullptr, S, Hq, 0, n_items);
-    } else {
-        hipLaunchKernelGGL((qknorm_rope_append_kernel<bf16_t, DenseRows>), dim3((unsigned)blocks), dim3(256), 0, st,
-                           (const bf16_t*)q, q_row_stride, (const bf16_t*)q_norm_w, (const bf16_t*)nullptr, eps,
-                           order, (const bf16_t*)cos, (const bf16_t*)sin, cs_stride, table_rows, positions,
-                           (bf16_t*)q_out, (bf16_t*)nullptr, (bf16_t*)nullptr, none, (const int32_t*)nullptr, S, Hq, 0,
-                           n_items);
-    }
+    if (dtype == CRANE_HIP_F32)
+        launch_append<float>(QkvRows<float>{(const float*)q, q_row_stride}, blocks, q_norm_w, nullptr, eps, order, cos,
+                             sin, cs_stride, table_rows, positions, q_out, nullptr, nullptr, none, nullptr, S, Hq, 0,
+                             n_items, st);
+    else
+        launch_append<bf16_t>(QkvRows<bf16_t>{(const bf16_t*)q, q_row_stride}, blocks, q_norm_w, nullptr, eps, order,
+                              cos, sin, cs_stride, table_rows, positions, q_out, nullptr, nullptr, none, nullptr, S, Hq,
+                              0, n_items, st);
     return launch_status(hipGetLastError());
 }
 
@@ -261,7 +377,10 @@ extern "C" int crane_hip_qknorm_rope_append_paged(const void* qkv, int64_t qkv_r
     const int rc = check_paged(n_pages, page_rows, block_table, table_stride, Hkv);
     if (rc) return rc;
     if ((int64_t)S > table_stride * page_rows) return CRANE_HIP_E_CAPACITY;
-    return qknorm_rope_append(qkv, qkv_row_stride, q_norm_w, k_norm_w, eps, order, cos, sin, cs_stride, table_rows,
+    RowSource src;
+    src.qkv = qkv;
+    src.stride = qkv_row_stride;
+    return qknorm_rope_append(src, q_norm_w, k_norm_w, eps, order, cos, sin, cs_stride, table_rows,
                               positions, q_out, k_pool, v_pool,
                               PagedRows{block_table, table_stride, n_pages, page_rows}, cache_len, B, S, Hq, Hkv, D,
                               dtype, stream);

@@ -128,7 +128,14 @@ class DecoderModel:
             q = ops.linear(h, w.qkv, w.qkv_bias).view(B, S, Hq * D)
             q = ops.q_norm_rope(q, self.cos, self.sin, positions, Hq, w.q_norm, eps, self.order)
         else:
-            qkv = ops.linear(h, w.qkv, w.qkv_bias).view(B, S, -1)
+            # a decode step's qkv_proj goes to the append as split-K partial
+            # products (ops.linear_for_append), reduced inside the append
+            if S == 1:
+                qkv = ops.linear_for_append(h, w.qkv, w.qkv_bias)
+                if not isinstance(qkv, ops.PartialProduct):
+                    qkv = qkv.view(B, S, -1)
+            else:
+                qkv = ops.linear(h, w.qkv, w.qkv_bias).view(B, S, -1)
             q = ops.qk_norm_rope_append(qkv, self.cos, self.sin, positions, self.k[a], self.v[a], self.lengths,
                                         bound, Hq, Hkv, w.q_norm, w.k_norm, eps, self.order)
         if S == 1:

@@ -42,10 +42,14 @@ def score_mode_code(score_mode: Optional[str], n_rep: int) -> int:
 
 
 def _dtype_code(t: torch.Tensor) -> int:
+    return _dtype_code_of(t.dtype)
+
+
+def _dtype_code_of(dtype: torch.dtype) -> int:
     try:
-        return _DTYPES[t.dtype]
+        return _DTYPES[dtype]
     except KeyError:
-        raise CraneHipError(_lib.E_DTYPE, f"dtype {t.dtype}") from None
+        raise CraneHipError(_lib.E_DTYPE, f"dtype {dtype}") from None
 
 
 def _dev(*ts: Optional[torch.Tensor]) -> torch.device:
@@ -130,14 +134,22 @@ def _rope_inputs(x: torch.Tensor, width: int, cos: torch.Tensor, sin: torch.Tens
     if W != width:
         raise CraneHipError(_lib.E_INVALID, f"{name} last dim {W} != {width}")
     _dtype_code(x)
+    if x.stride(2) != 1 or x.stride(0) != S * x.stride(1):
+        raise CraneHipError(_lib.E_INVALID, f"{name} rows must be dense with a unit inner stride")
+    _rope_tables(x.dtype, B, cos, sin, positions, q_norm_w, k_norm_w, order, name)
+    return dev, B, S
+
+
+def _rope_tables(dtype: torch.dtype, B: int, cos: torch.Tensor, sin: torch.Tensor, positions: torch.Tensor,
+                 q_norm_w: Optional[torch.Tensor], k_norm_w: Optional[torch.Tensor], order: str, name: str):
+    """The tables, norm weights, positions and order of a fused-rope call whose
+    rows are in `dtype`, for B sequences."""
     for t, n in ((cos, "cos"), (sin, "sin"), (q_norm_w, "q_norm_w"), (k_norm_w, "k_norm_w")):
-        if t is not None and t.dtype != x.dtype:
-            raise CraneHipError(_lib.E_DTYPE, f"{n} dtype {t.dtype} != {name} dtype {x.dtype}")
+        if t is not None and t.dtype != dtype:
+            raise CraneHipError(_lib.E_DTYPE, f"{n} dtype {t.dtype} != {name} dtype {dtype}")
     for t, n in ((q_norm_w, "q_norm_w"), (k_norm_w, "k_norm_w")):
         if t is not None and (t.numel() != HEAD_DIM or not t.is_contiguous()):
             raise CraneHipError(_lib.E_INVALID, f"{n} must be a contiguous [{HEAD_DIM}] weight")
-    if x.stride(2) != 1 or x.stride(0) != S * x.stride(1):
-        raise CraneHipError(_lib.E_INVALID, f"{name} rows must be dense with a unit inner stride")
     _contig(cos, "cos")
     _contig(sin, "sin")
     if cos.shape != sin.shape or cos.dim() != 2 or cos.shape[1] != HEAD_DIM // 2:
@@ -145,7 +157,6 @@ def _rope_inputs(x: torch.Tensor, width: int, cos: torch.Tensor, sin: torch.Tens
     _i32(positions, B, "positions")
     if order not in _ORDERS:
         raise CraneHipError(_lib.E_INVALID, f"order {order!r}")
-    return dev, B, S
 
 
 def qk_norm_rope_append(qkv: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,
@@ -160,8 +171,13 @@ def qk_norm_rope_append(qkv: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,
     Replaces qwen3/modeling.rs:382-423 + update_kv_cache's slice_set (:324-327);
     order "rope_then_norm" is Hunyuan's (hunyuan_dense/modeling.rs:541-555) and
     "rope_only" Qwen2.5's (qwen2.rs:75-76).  `max_rows` is a host-side bound
-    on cache_len[b] + S, checked against the cache capacity."""
+    on cache_len[b] + S, checked against the cache capacity.  qkv may be a
+    PartialProduct of the projection (linear_for_append): its splits are
+    summed (with its bias) and rounded in the same launch."""
     D = HEAD_DIM
+    if isinstance(qkv, PartialProduct):
+        return _qk_norm_rope_append_parts(qkv, cos, sin, positions, k_cache, v_cache, cache_len, max_rows, num_heads,
+                                          num_kv_heads, q_norm_w, k_norm_w, eps, order)
     dev, B, S = _rope_inputs(qkv, (num_heads + 2 * num_kv_heads) * D, cos, sin, positions, q_norm_w, k_norm_w, order)
     _dev(qkv, k_cache, v_cache, cache_len)
     if k_cache.shape != v_cache.shape or k_cache.dim() != 4 or k_cache.shape[0] != B or \
@@ -176,6 +192,39 @@ def qk_norm_rope_append(qkv: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,
     q_out = torch.empty((B, num_heads, S, D), dtype=qkv.dtype, device=dev)
     rc = _lib.lib().crane_hip_qknorm_rope_append(
         qkv.data_ptr(), qkv.stride(1), _ptr(q_norm_w), _ptr(k_norm_w), eps, _ORDERS[order],
+        cos.data_ptr(), sin.data_ptr(), cos.stride(0), cos.shape[0], positions.data_ptr(),
+        q_out.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), k_cache.shape[2],
+        cache_len.data_ptr(), max_rows, B, S, num_heads, num_kv_heads, D, dt, _stream(dev))
+    check(rc, "qk_norm_rope_append")
+    return q_out
+
+
+def _qk_norm_rope_append_parts(pp: "PartialProduct", cos, sin, positions, k_cache, v_cache, cache_len, max_rows,
+                               num_heads, num_kv_heads, q_norm_w, k_norm_w, eps, order) -> torch.Tensor:
+    D = HEAD_DIM
+    width = (num_heads + 2 * num_kv_heads) * D
+    parts = pp.parts
+    dev = _dev(parts, cos, sin, positions, q_norm_w, k_norm_w, k_cache, v_cache, cache_len, pp.bias)
+    B = positions.numel()
+    if parts.dim() != 3 or parts.dtype != torch.float32 or B < 1 or parts.shape[1] % B or parts.shape[2] != width:
+        raise CraneHipError(_lib.E_INVALID, f"partial products must be f32 [splits, B*S, {width}]")
+    sp, S = parts.shape[0], parts.shape[1] // B
+    _contig(parts, "parts")
+    dt = _dtype_code_of(pp.dtype)
+    _rope_tables(pp.dtype, B, cos, sin, positions, q_norm_w, k_norm_w, order, "qkv")
+    if pp.bias is not None and (pp.bias.dtype != pp.dtype or pp.bias.numel() != width or not pp.bias.is_contiguous()):
+        raise CraneHipError(_lib.E_INVALID, f"bias must be a contiguous [{width}] tensor of the rows' dtype")
+    if k_cache.shape != v_cache.shape or k_cache.dim() != 4 or k_cache.shape[0] != B or \
+            k_cache.shape[1] != num_kv_heads or k_cache.shape[3] != D:
+        raise CraneHipError(_lib.E_INVALID, "caches must be [B, Hkv, cap, D]")
+    for t, name in ((k_cache, "k_cache"), (v_cache, "v_cache")):
+        if t.dtype != pp.dtype:
+            raise CraneHipError(_lib.E_DTYPE, f"{name} dtype {t.dtype} != qkv dtype {pp.dtype}")
+        _contig(t, name)
+    _i32(cache_len, B, "cache_len")
+    q_out = torch.empty((B, num_heads, S, D), dtype=pp.dtype, device=dev)
+    rc = _lib.lib().crane_hip_qknorm_rope_append_parts(
+        parts.data_ptr(), sp, _ptr(pp.bias), _ptr(q_norm_w), _ptr(k_norm_w), eps, _ORDERS[order],
         cos.data_ptr(), sin.data_ptr(), cos.stride(0), cos.shape[0], positions.data_ptr(),
         q_out.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), k_cache.shape[2],
         cache_len.data_ptr(), max_rows, B, S, num_heads, num_kv_heads, D, dt, _stream(dev))
@@ -524,11 +573,12 @@ def release_stream(device: Optional[torch.device] = None, stream: Optional[torch
 
 class PartialProduct:
     """The f32 split-K partial products [splits, M, N] of a projection
-    (crane_gemm_linear_split) whose output only feeds add_rms_norm, which sums
-    them in split order and rounds once, as the whole product's output."""
+    (crane_gemm_linear_split) whose output only feeds add_rms_norm or
+    qk_norm_rope_append, which sum them in split order (adding `bias`, when
+    given, for the append) and round once, as the whole product's output."""
 
-    def __init__(self, parts: torch.Tensor, dtype: torch.dtype):
-        self.parts, self.dtype = parts, dtype
+    def __init__(self, parts: torch.Tensor, dtype: torch.dtype, bias: Optional[torch.Tensor] = None):
+        self.parts, self.dtype, self.bias = parts, dtype, bias
 
     @property
     def shape(self):
@@ -558,6 +608,28 @@ def linear_for_residual(x: torch.Tensor, weight: torch.Tensor):
                       "linear_split")
                 return PartialProduct(parts, x.dtype)
     return linear(x, weight)
+
+
+def linear_for_append(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor] = None):
+    """The merged qkv projection x [M, K] W^T (+ bias) of a decode step, whose
+    rows go only into qk_norm_rope_append: a PartialProduct of 2 splits when
+    the split applies (bf16, M <= 32; crane_gemm_split_supported), else
+    linear(x, weight, bias).  (2 splits: 12.5 against 13.5 us at Qwen3-8B's
+    qkv_proj and 32 rows; 4 splits took 15.4.)"""
+    dev = _dev(x, weight, bias)
+    K = x.shape[-1]
+    M = x.numel() // K
+    if x.dtype == torch.bfloat16 and weight.dim() == 2 and weight.shape[1] == K and weight.dtype == x.dtype and \
+            (bias is None or bias.dtype == x.dtype):
+        N = weight.shape[0]
+        if _lib.lib().crane_gemm_split_supported(M, N, K, 2, _lib.BF16):
+            _contig(x, "x")
+            _contig(weight, "weight")
+            parts = torch.empty((2, M, N), dtype=torch.float32, device=dev)
+            check(_lib.lib().crane_gemm_linear_split(_gemm(dev)._h, x.data_ptr(), weight.data_ptr(), parts.data_ptr(),
+                                                     M, N, K, 2, _lib.BF16, _stream(dev)), "linear_split")
+            return PartialProduct(parts, x.dtype, bias)
+    return linear(x, weight, bias)
 
 
 def _add_rms_norm_parts(residual: torch.Tensor, hidden: PartialProduct, weight: Optional[torch.Tensor],

@@ -109,6 +109,23 @@ int crane_hip_qknorm_rope_append(const void* qkv, int64_t qkv_row_stride,
                                  int64_t max_rows, int B, int S, int Hq, int Hkv, int D,
                                  int dtype, void* stream);
 
+/* crane_hip_qknorm_rope_append reading the merged projection's f32 split-K
+ * partial products instead of its output rows: parts [n_parts, B*S,
+ * (Hq+2*Hkv)*D] as crane_gemm_linear_split (crane_gemm.h) writes them,
+ * n_parts 2 or 4, and the projection's bias [(Hq+2*Hkv)*D] in `dtype` or NULL.
+ * Each row value is T(sum of the splits in split order + bias), the rounding
+ * point of the projection's own output (only the f32 summation order
+ * differs), then the same per-head arithmetic and cache writes.  For a
+ * decode step's qkv_proj, whose split form reads the activations fewer times
+ * per weight byte; its reduction costs no launch.  No counterpart in the
+ * reference (candle rounds each matmul's output).  Dense cache only. */
+int crane_hip_qknorm_rope_append_parts(const float* parts, int n_parts, const void* qkv_bias,
+                                       const void* q_norm_w, const void* k_norm_w, float eps, int order,
+                                       const void* cos, const void* sin, int64_t cs_stride, int64_t table_rows,
+                                       const int32_t* positions, void* q_out, void* k_cache, void* v_cache,
+                                       int64_t cache_cap, const int32_t* cache_len, int64_t max_rows, int B, int S,
+                                       int Hq, int Hkv, int D, int dtype, void* stream);
+
 /* Query-only QK-norm + RoPE for a layer that shares another layer's K/V:
  * Hunyuan's cross-layer attention (CLA) path, hunyuan_dense/modeling.rs:502-514,
  * which projects q alone, applies rope then query_layernorm, and attends over

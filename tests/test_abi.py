@@ -167,6 +167,37 @@ def test_append_argument_checks(kw, code):
     assert _append(**kw) == code
 
 
+def _append_parts(**kw):
+    a = dict(parts=16, n=2, bias=None, qw=None, kw=None, eps=1e-6, order=0, cos=16, sin=16, cs_stride=64,
+             rows=40960, pos=16, q_out=16, kc=16, vc=16, cap=4096, clen=16, max_rows=4096, B=32, S=1,
+             Hq=32, Hkv=8, D=128, dtype=1, stream=None)
+    a.update(kw)
+    return _lib.lib().crane_hip_qknorm_rope_append_parts(
+        a["parts"], a["n"], a["bias"], a["qw"], a["kw"], a["eps"], a["order"], a["cos"], a["sin"], a["cs_stride"],
+        a["rows"], a["pos"], a["q_out"], a["kc"], a["vc"], a["cap"], a["clen"], a["max_rows"], a["B"], a["S"],
+        a["Hq"], a["Hkv"], a["D"], a["dtype"], a["stream"])
+
+
+@pytest.mark.parametrize("kw,code", [
+    (dict(n=3), _lib.E_INVALID),               # 2 or 4 splits
+    (dict(n=1), _lib.E_INVALID),
+    (dict(n=3, S=0), _lib.E_INVALID),
+    (dict(dtype=3), _lib.E_DTYPE),
+    (dict(D=96), _lib.E_HEAD_DIM),
+    (dict(Hkv=5), _lib.E_GQA),
+    (dict(max_rows=4097), _lib.E_CAPACITY),
+    (dict(parts=None), _lib.E_INVALID),
+    (dict(parts=20), _lib.E_ALIGN),
+    (dict(bias=24), _lib.E_ALIGN),
+    (dict(cos=None), _lib.E_INVALID),
+    (dict(cs_stride=32), _lib.E_INVALID),
+    (dict(S=0), _lib.OK),
+    (dict(parts=None, B=0), _lib.OK),
+])
+def test_append_parts_argument_checks(kw, code):
+    assert _append_parts(**kw) == code
+
+
 def _qnorm(**kw):
     a = dict(q=16, stride=2048, qw=None, eps=1e-6, order=1, cos=16, sin=16, cs_stride=64, rows=40960, pos=16,
              q_out=16, B=1, S=2048, Hq=16, D=128, dtype=1, stream=None)

@@ -197,6 +197,51 @@ def test_append_parity(gpu, orc, name, B, S, Hq, Hkv, clen, posn, cap, order, dt
 
 
 @pytest.mark.parametrize("dtype", ["bf16", "f32"])
+@pytest.mark.parametrize("order", ["norm_then_rope", "rope_then_norm", "rope_only"])
+@pytest.mark.parametrize("splits,bias,B,S,Hq,Hkv", [(2, False, 32, 1, 32, 8), (2, True, 3, 5, 8, 2),
+                                                    (4, True, 32, 1, 32, 8), (4, False, 2, 3, 28, 4)])
+def test_append_parts_matches_rows(gpu, orc, splits, bias, B, S, Hq, Hkv, order, dtype):
+    """The append reading split-K partial products (a decode step's qkv_proj
+    as crane_gemm_linear_split writes them) gives, bit for bit, what the
+    rows path gives for the rows T(sum of the splits in split order + bias):
+    q, the K and V rows written and the canary rows left alone."""
+    from crane_amd import ops
+    note(f"append parts: {splits} splits, bias {bias}, B={B} S={S} Hq={Hq} Hkv={Hkv} {order} {dtype}")
+    cap, W = 16, (Hq + 2 * Hkv) * D
+    r = cases.rng(cases.SEED0 + 260 + splits + 3 * B + S)
+    parts = cases.normal(r, (splits, B * S, W)).astype(np.float32)
+    b = cases.cast(0.5 * cases.normal(r, (W,)), dtype) if bias else None
+    acc = np.zeros((B * S, W), np.float32)
+    for p in parts:
+        acc = (acc + p).astype(np.float32)
+    if b is not None:
+        acc = (acc + b).astype(np.float32)
+    qkv = cases.cast(acc, dtype).reshape(B, S, W)
+    qw = cases.cast(1 + 0.1 * cases.normal(r, (D,)), dtype)
+    kw = cases.cast(1 + 0.1 * cases.normal(r, (D,)), dtype)
+    cos, sin = orc.rope_tables(D, 1e6, 256)
+    cos, sin = cases.cast(cos, dtype), cases.cast(sin, dtype)
+    clen = [(3 * i) % (cap - S) for i in range(B)]
+    posn = [(5 * i + 1) % 200 for i in range(B)]
+    outs = []
+    for src in ("rows", "parts"):
+        kd = dev_t(np.full((B, Hkv, cap, D), 3.0, np.float32), dtype, gpu)
+        vd = dev_t(np.full((B, Hkv, cap, D), 3.0, np.float32), dtype, gpu)
+        if src == "rows":
+            x = dev_t(qkv, dtype, gpu)
+        else:
+            x = ops.PartialProduct(torch.from_numpy(parts).to(gpu), torch.bfloat16 if dtype == "bf16" else torch.float32,
+                                   None if b is None else dev_t(b, dtype, gpu))
+        q = ops.qk_norm_rope_append(x, dev_t(cos, dtype, gpu), dev_t(sin, dtype, gpu), i32(posn, gpu), kd, vd,
+                                    i32(clen, gpu), max(clen) + S, Hq, Hkv, dev_t(qw, dtype, gpu),
+                                    dev_t(kw, dtype, gpu), 1e-6, order)
+        torch.cuda.synchronize()
+        outs.append((host(q), host(kd), host(vd)))
+    for name, a, c in zip(("q", "k", "v"), outs[0], outs[1]):
+        assert np.array_equal(a, c), f"{name} differs between the rows and the partial products"
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "f32"])
 def test_cla_q_only_matches_the_append(gpu, orc, dtype):
     """Hunyuan's CLA layer: q alone through rope then query_layernorm, read
     from a narrowed [B, S, Hq*D] view of a wider row, equals the q rows of the

@@ -224,9 +224,10 @@ def _mlp_of(t):
 
 
 @pytest.mark.parametrize("family,L,cla,dims", [("qwen3", 3, 1, None), ("hunyuan", 4, 2, None), ("qwen2", 2, 1, None),
-                                               ("qwen3", 2, 1, (1024, 16, 4, 2048))],
-                         ids=["qwen3", "hunyuan", "qwen2", "qwen3-split-projections"])
-def test_stack_layer_by_layer(gpu, orc, family, L, cla, dims):
+                                               ("qwen3", 2, 1, (2048, 16, 4, 2048)),
+                                               ("qwen2", 2, 1, (2048, 16, 4, 2048))],
+                         ids=["qwen3", "hunyuan", "qwen2", "qwen3-split-projections", "qwen2-split-projections"])
+def test_stack_layer_by_layer(gpu, orc, family, L, cla, dims, monkeypatch):
     """Each layer of the stack at the one-layer bar: the oracle's layer i runs
     on the GPU's own input to layer i and over the GPU's cache rows of the
     earlier steps, so no earlier layer's error reaches it; then the final norm
@@ -236,9 +237,19 @@ def test_stack_layer_by_layer(gpu, orc, family, L, cla, dims):
     if dims is None:
         m, ref = _build(gpu, orc, family, L, cla)
     else:
-        # o_proj K = 2048, down_proj K = 2048: decode steps take the split-K projections
+        # qkv_proj, o_proj and down_proj all have K = 2048: decode steps take the
+        # split-K projections (qkv_proj's reduced, with Qwen2.5's bias, in the append)
         hidden, Hq, Hkv, inter = dims
         m, ref = _build(gpu, orc, family, L, cla, hidden=hidden, Hq=Hq, Hkv=Hkv, inter=inter)
+    from crane_amd import ops
+    qkv_split = []
+    real = ops.linear_for_append
+
+    def spy(*a, **k):
+        r = real(*a, **k)
+        qkv_split.append(isinstance(r, ops.PartialProduct))
+        return r
+    monkeypatch.setattr(ops, "linear_for_append", spy)
     r = cases.rng(177 + L)
     B, H = m.batch, m.cfg.hidden
     pos = np.array([0, 7], np.int32)
@@ -251,6 +262,8 @@ def test_stack_layer_by_layer(gpu, orc, family, L, cla, dims):
         assert len(trace) == L
         if dims is not None and S == 1:
             assert all(t[1].dim() == 3 for t in trace), "the decode step's down_proj ran split"
+            assert qkv_split and all(qkv_split), "the decode step's qkv_proj ran split into the append"
+        qkv_split.clear()
         res_in = x.reshape(B * S, H)
         for i in range(L):
             # the oracle's cache of the layer's anchor: the GPU's rows of the
