@@ -357,9 +357,11 @@ def bench_gemm(args, dev, stream, lib):
             log(f"[gemm {tag}] same product on constant inputs: {msc * 1e3:.1f} us, {tfc:.1f} TFLOP/s "
                 f"({tfc / BF16_PEAK_TFLOPS * 100:.1f}% of bf16 peak)")
         del x, ws_, b, y
-    # the decode step's o_proj and down_proj as the model driver runs them: f32
-    # partial products over 4 splits of K (summed by the add + norm that follows)
-    for tag, M, N, K, sp in (("c3_o_proj_split4", 32, 4096, 4096, 4), ("c3_down_proj_split4", 32, 4096, 12288, 4)):
+    # the decode step's qkv_proj, o_proj and down_proj as the model driver runs
+    # them: f32 partial products over 2 or 4 splits of K (summed by the append
+    # or the add + norm that follows)
+    for tag, M, N, K, sp in (("c3_qkv_proj_split2", 32, 6144, 4096, 2), ("c3_o_proj_split4", 32, 4096, 4096, 4),
+                             ("c3_down_proj_split4", 32, 4096, 12288, 4)):
         gen = torch.Generator(device=dev).manual_seed(SEED0 + 9)
         x = randn((M, K), gen, torch.bfloat16, dev)
         copies = max(1, -(-600_000_000 // (N * K * 2)))
@@ -472,6 +474,31 @@ def bench_read_ceiling(args, dev, stream):
             f"{gbs:.1f} GB/s ({gbs / HBM_PEAK_GBS * 100:.1f}% of HBM)")
         if best is None or gbs > best["gbs"]:
             best = dict(gbs=gbs, ms=ms, span_kib=16 * 256 * loads // 1024)
+    # One launch reading the bytes of one decode-step weight (Qwen3-8B shape,
+    # bf16), back to back over rotated slices of the buffers (> 600 MB in all,
+    # so every read comes from HBM): the rate a kernel of that size reaches
+    # with nothing but reads, its launch, ramp and drain included.  The
+    # fastest span of the three per size.
+    best["single_reads"] = {}
+    for name, n in (("o_proj", 4096 * 4096 * 2), ("qkv_proj", 6144 * 4096 * 2), ("down_proj", 12288 * 4096 * 2),
+                    ("gate_up", 24576 * 4096 * 2)):
+        n = n // 4096 * 4096
+        slots = [(b, off) for b in range(R) for off in range(0, nbytes - n + 1, n)]
+        top = None
+        for loads in (8, 16, 32):
+            def launch(i, loads=loads, n=n, slots=slots):
+                b, off = slots[i % len(slots)]
+                rc = probe.crane_probe_read(bufs[b].data_ptr() + off, n, sink.data_ptr(), loads, st)
+                if rc:
+                    raise RuntimeError(f"crane_probe_read failed: {rc}")
+            ms = timed(launch, args.steps, args.warmup, stream)
+            if top is None or ms < top[0]:
+                top = (ms, loads)
+        gbs = n / (top[0] * 1e-3) / 1e9
+        best["single_reads"][name] = dict(bytes=n, us=round(top[0] * 1e3, 2), gbs=round(gbs, 1),
+                                          span_kib=16 * 256 * top[1] // 1024)
+        log(f"[read ceiling] one read of {name}'s {n / 1e6:.1f} MB: {top[0] * 1e3:.2f} us, {gbs:.1f} GB/s "
+            f"({gbs / HBM_PEAK_GBS * 100:.1f}% of HBM)")
     del bufs
     torch.cuda.empty_cache()
     return best
@@ -926,10 +953,12 @@ def main():
                 "span_kib_per_workgroup": ceil["span_kib"], "bytes_per_launch": 320 * 1000 * 1000,
                 "decode_frac_of_ceiling": round(dec["gbs"] / ceil["gbs"], 4),
                 "decode_p50_frac_of_ceiling": round(line["value_p50"] / ceil["gbs"], 4),
+                "single_reads": ceil["single_reads"],
                 "note": "a read-only stream with the decode kernel's access pattern and load form "
                         "(crane_amd/csrc/probe/hbm_probe.hip, a measurement helper outside the library: one "
                         "workgroup per contiguous span, all its loads in flight), 3 rotated 320 MB buffers; the "
-                        "decode roofline's peak stays the 8 TB/s datasheet figure"}
+                        "decode roofline's peak stays the 8 TB/s datasheet figure; single_reads: one launch reading "
+                        "one decode-step weight's bytes (Qwen3-8B shape), back to back from HBM"}
     if pre is not None:
         pre_obj = {"metric": "prefill attn TFLOP/s (c4: Qwen2.5-7B shape, B=8, S=4096, 28/4 heads, causal, bf16)",
                    "value": round(pre["tflops"], 2), "unit": "TFLOP/s", "ms_per_step": round(pre["ms"], 4),

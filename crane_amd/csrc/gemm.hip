@@ -246,8 +246,8 @@ int launch_skinny(const bf16_t* x, const bf16_t* w, const bf16_t* bias, bf16_t* 
 //                      384 of 64 42.2 us)
 // down_proj's shape [4096, 12288] stays on hipBLASLt through
 // crane_gemm_linear (26 us against 29); split over 4 ranges of K with 64
-// features per workgroup (crane_gemm_linear_split, 2 waves and a ring of 3
-// slots) it takes 19.3 us, and o_proj (4 waves, a ring of 2) 9.5 us.
+// features per workgroup (crane_gemm_linear_split, 1 wave and a ring of 3
+// slots) it takes 18.4 us, and o_proj (2 waves, a ring of 2) 8.6 us.
 
 constexpr int kRingMaxK = 8192;
 
@@ -524,34 +524,68 @@ int launch_ring(const RingCfg& c, const bf16_t* x, const bf16_t* w, const bf16_t
     return launch_status(hipGetLastError());
 }
 
-// Split-K partial products (decode rows, M <= 32): 64 features (FT 4) per
-// workgroup, K cut into `splits` ranges over gridDim.y, each wave's part of
-// its range walked in 128-wide stages through a ring of its own.  Two forms,
-// one workgroup per CU either way: 2 waves and a ring of 3 slots (96 KiB of
-// LDS) when each wave's stage count is a multiple of 3, else 4 waves and a
-// ring of 2 (128 KiB).  (The ring loop needs the stage count a multiple of
-// the depth; 4 slots of FT 4 would pass the 6-bit vmcnt.)  Qwen3-8B down_proj
-// [4096 x 12288] in 4 splits: 20.0 -> 19.4 us with the ring of 3; o_proj
-// [4096 x 4096] (4 stages per wave) keeps the ring of 2.  The ring depth of
-// the form a shape takes, or 0 when the shape does not split this way.
-int split_ring_depth(int64_t M, int64_t N, int64_t K, int64_t splits) {
-    if (M < 1 || M > kSkMaxM || N < 64 || N % 64 || N > 0x7fffffff || splits < 2 || splits > 16) return 0;
-    if (K % (splits * 4 * 256)) return 0;  // whole ring turns: 2 stages of 128 per wave
-    if (K / splits / 4 > kRingMaxK || 16LL * 4 * K * 2 > 0xffffffffLL) return 0;
-    const int64_t nst2 = K / splits / 2 / 128;  // stages per wave with 2 waves
-    return nst2 % 3 == 0 && K / splits / 2 <= kRingMaxK ? 3 : 2;
+// Split-K partial products (decode rows, M <= 32): K cut into `splits`
+// ranges over gridDim.y; a workgroup of KS waves takes 16 FT features of one
+// range, each wave its part of the range walked in 128-wide stages through a
+// ring of D slots of its own.  The shape sets the form:
+//   FT: 4, 3 or 2, the one whose busiest CU streams the fewest 16-feature
+//       tiles, ceil(N / (16 FT) * splits / 256) * FT, the widest on a tie;
+//   KS: 1 wave when a range holds at least 3072 of K, else 2;
+//   D:  3 when each wave's stage count is a multiple of 3, else 2.
+// (The ring loop needs the stage count a multiple of the depth and at least
+// 2; the (D - 1) stages in flight fit the 6-bit vmcnt.)  Qwen3-8B at 32 rows,
+// same-box sweep of these and 4-wave forms, back to back with the weights
+// read from HBM: qkv_proj [6144 x 4096] in 2 splits 12.7 -> 10.7 us (FT 3 and
+// 2 waves: 256 workgroups, where 64 features and 4 waves left 64 of the 256
+// CUs idle), o_proj [4096 x 4096] in 4 splits 9.4 -> 8.6 us (2 waves against
+// 4), down_proj [4096 x 12288] in 4 splits 19.3 -> 18.4 us (1 wave and a ring
+// of 3 against 2 waves).  {0, 0, 0} when the shape does not split this way.
+RingCfg split_cfg(int64_t M, int64_t N, int64_t K, int64_t splits) {
+    if (M < 1 || M > kSkMaxM || N < 32 || N > 0x7fffffff || K < 1 || splits < 2 || splits > 16 || K % splits)
+        return {0, 0, 0};
+    const int64_t kp = K / splits;
+    if (kp > 32768) return {0, 0, 0};
+    RingCfg c{0, 0, 0};
+    int64_t best = 0;
+    for (const int ft : {4, 3, 2}) {
+        if (N % (16 * ft)) continue;
+        const int64_t load = (N / (16 * ft) * splits + kRingCUs - 1) / kRingCUs * ft;
+        if (!c.ft || load < best) c.ft = ft, best = load;
+    }
+    if (!c.ft) return {0, 0, 0};
+    c.ks = kp >= 3072 ? 1 : 2;
+    if (kp % (256 * c.ks)) return {0, 0, 0};  // an even number of 128-wide stages per wave
+    c.d = kp / c.ks / 128 % 3 == 0 ? 3 : 2;
+    return c;
+}
+
+template <int MT, int KS, int D>
+void launch_split_ft(int ft, dim3 grid, const bf16_t* x, const bf16_t* w, float* part, int M, int N, int K,
+                     hipStream_t st) {
+    const dim3 block(64 * KS);
+    if (ft == 4)
+        hipLaunchKernelGGL((ring_gemm_kernel<MT, KS, D, 4, false, false, true>), grid, block, 0, st, x, w, nullptr,
+                           nullptr, M, N, K, part);
+    else if (ft == 3)
+        hipLaunchKernelGGL((ring_gemm_kernel<MT, KS, D, 3, false, false, true>), grid, block, 0, st, x, w, nullptr,
+                           nullptr, M, N, K, part);
+    else
+        hipLaunchKernelGGL((ring_gemm_kernel<MT, KS, D, 2, false, false, true>), grid, block, 0, st, x, w, nullptr,
+                           nullptr, M, N, K, part);
 }
 
 template <int MT>
-void launch_split(const bf16_t* x, const bf16_t* w, float* part, int M, int N, int K, int splits, int depth,
+void launch_split(const RingCfg& c, const bf16_t* x, const bf16_t* w, float* part, int M, int N, int K, int splits,
                   hipStream_t st) {
-    const dim3 grid((unsigned)(N / 64), (unsigned)splits);
-    if (depth == 3)
-        hipLaunchKernelGGL((ring_gemm_kernel<MT, 2, 3, 4, false, false, true>), grid, dim3(128), 0, st, x, w, nullptr,
-                           nullptr, M, N, K, part);
+    const dim3 grid((unsigned)(N / (16 * c.ft)), (unsigned)splits);
+    if (c.ks == 1 && c.d == 3)
+        launch_split_ft<MT, 1, 3>(c.ft, grid, x, w, part, M, N, K, st);
+    else if (c.ks == 1)
+        launch_split_ft<MT, 1, 2>(c.ft, grid, x, w, part, M, N, K, st);
+    else if (c.d == 3)
+        launch_split_ft<MT, 2, 3>(c.ft, grid, x, w, part, M, N, K, st);
     else
-        hipLaunchKernelGGL((ring_gemm_kernel<MT, 4, 2, 4, false, false, true>), grid, dim3(256), 0, st, x, w, nullptr,
-                           nullptr, M, N, K, part);
+        launch_split_ft<MT, 2, 2>(c.ft, grid, x, w, part, M, N, K, st);
 }
 
 struct Plan {
@@ -735,7 +769,7 @@ extern "C" int crane_gemm_linear_silu_mul(crane_gemm* g, const void* x, const vo
 }
 
 extern "C" int crane_gemm_split_supported(int64_t M, int64_t N, int64_t K, int splits, int dtype) {
-    return dtype == CRANE_HIP_BF16 && crane::split_ring_depth(M, N, K, splits) != 0;
+    return dtype == CRANE_HIP_BF16 && crane::split_cfg(M, N, K, splits).ft != 0;
 }
 
 extern "C" int crane_gemm_linear_split(crane_gemm* g, const void* x, const void* w, float* part, int64_t M, int64_t N,
@@ -747,14 +781,15 @@ extern "C" int crane_gemm_linear_split(crane_gemm* g, const void* x, const void*
     if (M == 0) return CRANE_HIP_OK;
     if (!x || !w || !part) return CRANE_HIP_E_INVALID;
     if (!crane::aligned16(x) || !crane::aligned16(w) || !crane::aligned16(part)) return CRANE_HIP_E_ALIGN;
-    const int depth = dtype == CRANE_HIP_BF16 ? crane::split_ring_depth(M, N, K, splits) : 0;
-    if (!depth) return CRANE_HIP_E_INVALID;
+    if (dtype != CRANE_HIP_BF16) return CRANE_HIP_E_INVALID;
+    const crane::RingCfg c = crane::split_cfg(M, N, K, splits);
+    if (!c.ft) return CRANE_HIP_E_INVALID;
     hipStream_t st = (hipStream_t)stream;
     if (M <= 16)
-        crane::launch_split<1>((const crane::bf16_t*)x, (const crane::bf16_t*)w, part, (int)M, (int)N, (int)K, splits,
-                               depth, st);
+        crane::launch_split<1>(c, (const crane::bf16_t*)x, (const crane::bf16_t*)w, part, (int)M, (int)N, (int)K,
+                               splits, st);
     else
-        crane::launch_split<2>((const crane::bf16_t*)x, (const crane::bf16_t*)w, part, (int)M, (int)N, (int)K, splits,
-                               depth, st);
+        crane::launch_split<2>(c, (const crane::bf16_t*)x, (const crane::bf16_t*)w, part, (int)M, (int)N, (int)K,
+                               splits, st);
     return crane::launch_status(hipGetLastError());
 }

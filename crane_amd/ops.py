@@ -614,8 +614,8 @@ def linear_for_append(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torc
     """The merged qkv projection x [M, K] W^T (+ bias) of a decode step, whose
     rows go only into qk_norm_rope_append: a PartialProduct of 2 splits when
     the split applies (bf16, M <= 32; crane_gemm_split_supported), else
-    linear(x, weight, bias).  (2 splits: 12.5 against 13.5 us at Qwen3-8B's
-    qkv_proj and 32 rows; 4 splits took 15.4.)"""
+    linear(x, weight, bias).  (2 splits: 10.7 us at Qwen3-8B's qkv_proj and
+    32 rows, against 13.7 for linear and 11.7 with 4 splits.)"""
     dev = _dev(x, weight, bias)
     K = x.shape[-1]
     M = x.numel() // K

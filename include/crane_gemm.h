@@ -78,8 +78,9 @@ int crane_gemm_linear_silu_mul(crane_gemm* g, const void* x, const void* w, void
                                int64_t K, int dtype, void* stream);
 
 /* 1 when crane_gemm_linear_split takes the shape, else 0: bf16, M <= 32 token
- * rows, N a multiple of 64, K a multiple of 1024 * splits with K / splits <=
- * 32768, 2 <= splits <= 16. */
+ * rows, N a multiple of 32, 2 <= splits <= 16, and K a multiple of splits
+ * whose share K / splits is at most 32768 and a multiple of 512 (of 256 from
+ * 3072 up). */
 int crane_gemm_split_supported(int64_t M, int64_t N, int64_t K, int splits, int dtype);
 
 /* The f32 partial products of a projection whose output only feeds a
@@ -87,9 +88,11 @@ int crane_gemm_split_supported(int64_t M, int64_t N, int64_t K, int splits, int 
  * splits) of x[M, K] W[N, K]^T, unrounded, no bias.  The sum over s in split
  * order, rounded once to T, is crane_gemm_linear's output up to the f32
  * summation order; crane_hip_add_rms_norm_parts (crane_layer.h) consumes it.
- * Each workgroup covers 64 output features over one split of K, so a decode
- * step's narrow products (o_proj, down_proj) read x splits times less per
- * weight byte than crane_gemm_linear's kernels.  No counterpart in the
+ * Each workgroup covers 32, 48 or 64 output features over one split of K
+ * (the width that spreads the workgroups most evenly over the CUs), so a
+ * decode step's narrow products (qkv_proj, o_proj, down_proj) fill the chip
+ * and read x splits times less per weight byte than crane_gemm_linear's
+ * kernels.  No counterpart in the
  * reference (candle rounds each matmul's output); part is 16-byte aligned
  * and holds splits * M * N floats.  CRANE_HIP_E_INVALID for a shape
  * crane_gemm_split_supported rejects. */

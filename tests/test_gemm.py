@@ -177,18 +177,24 @@ def test_linear_ring_parity(gpu, orc, M, N, K, bias):
 
 def test_split_shape_query():
     """Which shapes the split-K partial products take (host logic, no GPU):
-    bf16, at most 32 token rows, N a multiple of 64, K a multiple of 1024 per
-    split with at most 32768 per split, 2 to 16 splits."""
+    bf16, at most 32 token rows, N a multiple of 32, K a multiple of the
+    splits with a share of at most 32768 that is a multiple of 512 (of 256
+    from 3072 up: one wave a workgroup), 2 to 16 splits."""
     from crane_amd import _lib
     q = _lib.lib().crane_gemm_split_supported
     BF16, F32 = 1, 0
     assert q(32, 4096, 4096, 4, BF16) == 1    # Qwen3-8B decode o_proj
     assert q(32, 4096, 12288, 4, BF16) == 1   # ... and down_proj
     assert q(1, 64, 2048, 2, BF16) == 1
-    assert q(32, 4096, 4096, 3, BF16) == 0    # K not a multiple of 1024 per split
-    assert q(32, 4096, 2048, 4, BF16) == 0    # 512 per split: less than a ring turn per wave
+    assert q(32, 6144, 4096, 2, BF16) == 1    # ... and qkv_proj
+    assert q(32, 4096, 4096, 3, BF16) == 0    # K not a multiple of the splits
+    assert q(32, 4096, 2048, 4, BF16) == 1    # 512 per split: one ring turn of 2 waves
+    assert q(32, 4096, 1024, 4, BF16) == 0    # 256 per split: less than a ring turn
+    assert q(32, 4096, 3840, 2, BF16) == 0    # 1920 per split (2 waves): not a multiple of 512
+    assert q(32, 4096, 6656, 2, BF16) == 1    # 3328 per split (1 wave): a multiple of 256
     assert q(33, 4096, 4096, 4, BF16) == 0    # more token rows than the kernel takes
-    assert q(32, 4100, 4096, 4, BF16) == 0    # N not a multiple of 64
+    assert q(32, 4100, 4096, 4, BF16) == 0    # N not a multiple of 32
+    assert q(32, 4112, 4096, 4, BF16) == 0    # ... nor this one
     assert q(32, 4096, 4096, 1, BF16) == 0    # no split
     assert q(32, 4096, 4096, 4, F32) == 0
     assert q(32, 4096, 65536, 2, BF16) == 1   # 32768 per split: the limit
@@ -198,13 +204,16 @@ def test_split_shape_query():
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("M,N,K,splits", [
-    (32, 4096, 4096, 4),    # o_proj at the c3 decode batch: 64 workgroups x 4 splits
-    (32, 4096, 12288, 4),   # down_proj at c3: 2 waves, 12 stages a wave through a ring of 3
-    (5, 1024, 2048, 2),     # one token group; one ring turn a wave
+    (32, 4096, 4096, 4),    # o_proj at the c3 decode batch: 64 workgroups of 64 features x 4 splits, 2 waves
+    (32, 4096, 12288, 4),   # down_proj at c3: 1 wave, 24 stages through a ring of 3
+    (32, 6144, 4096, 2),    # qkv_proj at c3: 128 workgroups of 48 features x 2 splits
+    (5, 1024, 2048, 2),     # one token group, 32 features a workgroup; one ring turn a wave
     (17, 256, 8192, 8),     # a partial second token group, 8 splits
     (1, 640, 3072, 3),      # one token row, 3 splits
-    (9, 512, 6144, 2),      # one token group, ring of 3
-    (20, 320, 9216, 3),     # a partial second token group, 5 feature tiles, ring of 3
+    (9, 512, 6144, 2),      # one token group, 1 wave, ring of 3
+    (20, 320, 9216, 3),     # a partial second token group, 10 feature tiles, 1 wave, ring of 3
+    (11, 336, 3072, 2),     # 48 features, 2 waves, ring of 3
+    (24, 48, 8192, 2),      # one 48-feature tile, 1 wave, ring of 2
 ])
 def test_linear_split_parity(gpu, orc, M, N, K, splits):
     """The f32 partial products of crane_gemm_linear_split, summed in split
