@@ -78,7 +78,7 @@ int crane_gemm_linear_silu_mul(crane_gemm* g, const void* x, const void* w, void
                                int64_t K, int dtype, void* stream);
 
 /* 1 when crane_gemm_linear_split takes the shape, else 0: bf16, M <= 32 token
- * rows, N a multiple of 32, 2 <= splits <= 16, and K a multiple of splits
+ * rows, N a multiple of 32 or 48, 2 <= splits <= 16, and K a multiple of splits
  * whose share K / splits is at most 32768 and a multiple of 512 (of 256 from
  * 3072 up). */
 int crane_gemm_split_supported(int64_t M, int64_t N, int64_t K, int splits, int dtype);

@@ -177,7 +177,7 @@ def test_linear_ring_parity(gpu, orc, M, N, K, bias):
 
 def test_split_shape_query():
     """Which shapes the split-K partial products take (host logic, no GPU):
-    bf16, at most 32 token rows, N a multiple of 32, K a multiple of the
+    bf16, at most 32 token rows, N a multiple of 32 or 48, K a multiple of the
     splits with a share of at most 32768 that is a multiple of 512 (of 256
     from 3072 up: one wave a workgroup), 2 to 16 splits."""
     from crane_amd import _lib
@@ -193,8 +193,9 @@ def test_split_shape_query():
     assert q(32, 4096, 3840, 2, BF16) == 0    # 1920 per split (2 waves): not a multiple of 512
     assert q(32, 4096, 6656, 2, BF16) == 1    # 3328 per split (1 wave): a multiple of 256
     assert q(33, 4096, 4096, 4, BF16) == 0    # more token rows than the kernel takes
-    assert q(32, 4100, 4096, 4, BF16) == 0    # N not a multiple of 32
-    assert q(32, 4112, 4096, 4, BF16) == 0    # ... nor this one
+    assert q(32, 4100, 4096, 4, BF16) == 0    # N not a multiple of 32 or 48
+    assert q(32, 4112, 4096, 4, BF16) == 0    # ... nor of 48
+    assert q(32, 144, 4096, 4, BF16) == 1     # 3 tiles of 48 features
     assert q(32, 4096, 4096, 1, BF16) == 0    # no split
     assert q(32, 4096, 4096, 4, F32) == 0
     assert q(32, 4096, 65536, 2, BF16) == 1   # 32768 per split: the limit
@@ -331,6 +332,49 @@ def test_random_decode_linear(gpu, orc, i):
     assert_linear_close(got.float().cpu().numpy(), x, w, b, "bf16", orc, f"random linear {M}x{N}x{K}")
     got2 = ops.linear(_t(x, "bf16", gpu), _t(w, "bf16", gpu), _t(b, "bf16", gpu) if bias else None)
     assert bool((got == got2).all())
+
+
+def split_draw(seed: int, i: int):
+    """Draw i of the randomised split-K sweep: (M, N, K, splits) that
+    crane_gemm_split_supported takes, cycling over the feature widths (N a
+    multiple of 64, of 48, of 32) and the two wave counts (a share of K below
+    3072, a multiple of 512, takes 2 waves; from 3072, a multiple of 256, 1),
+    with M N K at most 1.5e9."""
+    r = cases.rng(seed + 9700 + i)
+    M = int(r.integers(1, 33))
+    splits = int(r.choice([2, 3, 4, 6, 8]))
+    base = (64, 48, 32)[i % 3]
+    N = base * int(r.integers(1, 129))
+    share = 512 * int(r.integers(1, 6)) if (i // 3) % 2 == 0 else 256 * int(r.integers(12, 33))
+    while M * N * splits * share > 1.5e9 and N > base:
+        N -= base
+    return M, N, splits * share, splits
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("i", range(N_RANDOM))
+def test_random_linear_split(gpu, orc, i):
+    """Random shapes of the split-K partial products, summed in split order
+    and rounded once, against the oracle at the bar of
+    test_linear_split_parity; a second call repeats the bits."""
+    import torch
+    from crane_amd import _lib, ops
+    M, N, K, splits = split_draw(SEED, i)
+    print(f"random linear split {i} (seed {SEED}): M={M} N={N} K={K} splits={splits}", flush=True)
+    assert _lib.lib().crane_gemm_split_supported(M, N, K, splits, _lib.BF16) == 1
+    x, w, _ = _case(SEED + 9800 + i, M, N, K, "bf16", False)
+    xd, wd = _t(x, "bf16", gpu), _t(w, "bf16", gpu)
+    outs = []
+    for _ in range(2):
+        parts = torch.empty((splits, M, N), dtype=torch.float32, device=gpu)
+        assert _lib.lib().crane_gemm_linear_split(ops._gemm(gpu)._h, xd.data_ptr(), wd.data_ptr(), parts.data_ptr(),
+                                                  M, N, K, splits, _lib.BF16, ops._stream(gpu)) == 0
+        outs.append(parts.cpu().numpy())
+    assert np.array_equal(outs[0], outs[1])
+    acc = np.zeros((M, N), np.float32)
+    for p in outs[0]:
+        acc = (acc + p).astype(np.float32)
+    assert_linear_close(cases.bf16(acc), x, w, None, "bf16", orc, f"random split linear {M}x{N}x{K}/{splits}")
 
 
 def silu_mul_draw(seed: int, i: int):
