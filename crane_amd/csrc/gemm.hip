@@ -13,8 +13,9 @@
 // lm_head) take the per-wave ring kernel below; other wide ones (N >= 16384)
 // the streaming kernel; the rest, down_proj among them, hipBLASLt.  A
 // product whose output only feeds a residual add (a decode step's o_proj and
-// down_proj) can instead leave f32 split-K partial products for the add +
-// norm to sum (crane_gemm_linear_split: the ring kernel's PARTIAL form).  The
+// down_proj) or the fused append (its qkv_proj) can instead leave f32 split-K
+// partial products for the add + norm or the append to sum
+// (crane_gemm_linear_split: the ring kernel's PARTIAL form).  The
 // streaming kernel (measured at the Qwen3-8B decode shapes before the ring
 // kernel: gate_up [24576, 4096] 43 us vs hipBLASLt's 47 us, lm_head
 // [151936, 4096] 241 us vs ~355 us):

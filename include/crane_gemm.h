@@ -84,10 +84,12 @@ int crane_gemm_linear_silu_mul(crane_gemm* g, const void* x, const void* w, void
 int crane_gemm_split_supported(int64_t M, int64_t N, int64_t K, int splits, int dtype);
 
 /* The f32 partial products of a projection whose output only feeds a
- * residual add: part[s][M][N] = sum over k in [s K / splits, (s + 1) K /
- * splits) of x[M, K] W[N, K]^T, unrounded, no bias.  The sum over s in split
- * order, rounded once to T, is crane_gemm_linear's output up to the f32
- * summation order; crane_hip_add_rms_norm_parts (crane_layer.h) consumes it.
+ * residual add or the fused append: part[s][M][N] = sum over k in
+ * [s K / splits, (s + 1) K / splits) of x[M, K] W[N, K]^T, unrounded, no
+ * bias.  The sum over s in split order, rounded once to T, is
+ * crane_gemm_linear's output up to the f32 summation order;
+ * crane_hip_add_rms_norm_parts (crane_layer.h) and
+ * crane_hip_qknorm_rope_append_parts (crane_hip.h) consume it.
  * Each workgroup covers 32, 48 or 64 output features over one split of K
  * (the width that spreads the workgroups most evenly over the CUs), so a
  * decode step's narrow products (qkv_proj, o_proj, down_proj) fill the chip
